@@ -1,0 +1,157 @@
+/* noise_amd — C ABI of the MI355X (gfx950) kernels behind Noise's forward-only population training hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as void*), launches on that stream
+ * without synchronizing, allocates nothing, and returns 0 or a NOISE_ERR_* code; noise_last_error() then holds a
+ * message. Tensors are contiguous row-major unless a stride argument says otherwise. "bf16" buffers are uint16_t
+ * bfloat16 bit patterns. Citations are relative to the reference checkout (qlabs-eng/noise).
+ */
+#ifndef NOISE_AMD_H
+#define NOISE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NOISE_OK 0
+#define NOISE_ERR_ARG 1   /* bad shape, size, pointer or configuration: Python raises ValueError */
+#define NOISE_ERR_HIP 2   /* a HIP runtime call failed: Python raises RuntimeError */
+#define NOISE_ERR_WORKSPACE 3 /* workspace too small: Python raises ValueError */
+
+#define NOISE_MAX_LAYERS 16
+
+/* Message of the last failed call on this thread. */
+const char* noise_last_error(void);
+/* ABI version (bumped on any signature change). */
+int noise_abi_version(void);
+
+/* ---- a1: counter-based noise (replaces the 2^28-value torch.randn buffer and the torch.randint offsets) -------- */
+
+/* out[j] = G[start + j], the virtual N(0,1) buffer of Philox4x32-10 + Box-Muller values.
+ * Replaces: archive/10M/train/val/eggroll.py:114 (torch.randn(NOISE, generator=manual_seed(SEED))). */
+int noise_rng_buffer(uint64_t seed, uint64_t start, int64_t n, float* out, void* stream);
+
+/* out[p * pairs + d] = offset of direction d of parameter p at this step, an integer in [0, 2^28 - widths[p]);
+ * widths (host array [n_params]) = sum(shape) of each parameter in named_parameters() order.
+ * Replaces: archive/10M/train/val/eggroll.py:117-120 (Eggroll.offsets). */
+int noise_rng_offsets(uint64_t seed, uint64_t step, const int64_t* widths, int32_t n_params, int64_t pairs,
+                      int64_t* out, void* stream);
+
+/* rows[j, col0[p] + e] = G[offsets[p * pairs + directions[j]] + e] for e < widths[p]: the noise of n directions,
+ * every parameter's (a | b) slice side by side (col0 = prefix sums of widths, row stride = sum of widths); widths is
+ * a host array; a direction outside [0, pairs) yields a row of NaN.
+ * Replaces: archive/10M/train/val/eggroll.py:122-128 (Eggroll.noise). */
+int noise_rng_rows(uint64_t seed, const int64_t* offsets, int64_t pairs, const int64_t* widths, int32_t n_params,
+                   const int64_t* directions, int64_t n, float* rows, void* stream);
+
+/* ---- a2: perturbed linear --------------------------------------------------------------------------------- */
+
+/* y[i, t, :] = x[i, t, :] W^T + sign[i] (x[i, t, :] . b_i) a_i, a_i = noise[i * noise_stride + a_off + (0..out)],
+ * b_i = noise[i * noise_stride + b_off + (0..in)]; x bf16 [m, T, in] (x_shared != 0: one [T, in] for every member),
+ * W bf16 [out, in]. Outputs (either may be NULL): y fp32 [m, T, out]; sumsq fp32 [m] = sum of y^2 per member.
+ * T % 128 == 0, in % 64 == 0, out % 128 == 0.
+ * Replaces: archive/10M/train/val/eggroll.py:56-58 (lowrank). */
+int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t* w, const float* noise, int64_t noise_stride,
+                  int64_t a_off, int64_t b_off, const float* sign, int64_t m, int64_t T, int64_t in, int64_t out,
+                  float* y, float* sumsq, void* workspace, size_t workspace_bytes, void* stream);
+size_t noise_lowrank_workspace(int64_t m, int64_t T, int64_t in, int64_t out, int32_t x_shared);
+
+/* ---- a5: windowed causal attention ------------------------------------------------------------------------ */
+
+/* out[b, t, h, :] = softmax_s(q[b,t,h] . k[b,s,h] / 8 over 0 <= t - s <= window) v[b, s, h, :]; q/k/v/out bf16 with
+ * strides (batch, token) in elements and heads of 64 channels side by side (head h at +64 h); T % 64 == 0.
+ * lse (optional, fp32 [batch, heads, T]) receives the log-sum-exp of each query's logits.
+ * Replaces: utils/model.py:17-31 (attention / window_mask, flex_attention). */
+int noise_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t batch, int32_t heads, int64_t T,
+                    int64_t stride_b, int64_t stride_t, int32_t window, uint16_t* out, int64_t out_stride_b,
+                    int64_t out_stride_t, float* lse, void* stream);
+
+/* ---- a3, a4, a6: the perturbed population forward of the fixed GPT ---------------------------------------- */
+
+typedef struct noise_layer {
+  const uint16_t* w_qkv;      /* bf16 [1536, 512]: c_q, c_k, c_v rows stacked (nn.Linear [out, in]) */
+  const uint16_t* w_proj;     /* bf16 [512, 512]  attn.c_proj */
+  const uint16_t* w_fc;       /* bf16 [2048, 512] mlp.c_fc */
+  const uint16_t* w_mlp_proj; /* bf16 [512, 2048] mlp.c_proj */
+  const float* w_gate;        /* fp32 [8, 32] attn.ve_gate, NULL on blocks without value embeddings */
+  const float* ve;            /* fp32 [padded_vocab, 512] value_embeds.{i}, NULL likewise */
+  int32_t window;             /* left window of the causal attention */
+} noise_layer;
+
+typedef struct noise_gpt {
+  int32_t n_layer;
+  int32_t vocab;              /* logits used by the loss (GPTConfig.vocab_size) */
+  int32_t padded_vocab;       /* rows of wte / lm_head / value tables, multiple of 128 */
+  const float* resid_lambdas; /* fp32 [n_layer] */
+  const float* x0_lambdas;    /* fp32 [n_layer] */
+  const float* wte;           /* fp32 [padded_vocab, 512] */
+  const uint16_t* lm_head;    /* bf16 [padded_vocab, 512] */
+  const float* rope_cos;      /* fp32 [T, 32]: the bf16 rotary table's values (utils/model.py:177-183) */
+  const float* rope_sin;
+  noise_layer layers[NOISE_MAX_LAYERS];
+} noise_gpt;
+
+/* Where each parameter's (a | b) slice (eps for the lambdas) sits in a noise row. rows == NULL: no perturbation. */
+typedef struct noise_perturbation {
+  const float* rows;          /* fp32 [n_rows, stride] */
+  int64_t stride;
+  int64_t resid_lambdas, x0_lambdas, wte, lm_head;
+  int64_t c_q[NOISE_MAX_LAYERS], c_k[NOISE_MAX_LAYERS], c_v[NOISE_MAX_LAYERS], c_proj[NOISE_MAX_LAYERS];
+  int64_t ve_gate[NOISE_MAX_LAYERS], c_fc[NOISE_MAX_LAYERS], mlp_proj[NOISE_MAX_LAYERS], ve[NOISE_MAX_LAYERS];
+} noise_perturbation;
+
+/* Evaluates `members` perturbed models, member i on token row member_seq[i] with noise row member_row[i] scaled by
+ * member_sign[i] (+-sigma), T tokens each (T % 128 == 0). tokens / targets int64 [n_seq, T]; a target < 0 is ignored.
+ * Outputs (each may be NULL): loss_sum fp32 [members] = summed next-token CE of each member; token_loss fp32
+ * [members, T]; logits fp32 [members, T, vocab] (soft-capped, 15 tanh(z / 15)).
+ * workspace: noise_population_forward_workspace(members, T) bytes of device memory.
+ * Replaces: archive/10M/train/val/eggroll.py:66-103 (population_loss) and, with rows == NULL,
+ * utils/model.py:193-210 (GPT.forward). */
+size_t noise_population_forward_workspace(int64_t members, int64_t T);
+int noise_population_forward(const noise_gpt* model, const noise_perturbation* pert, const int64_t* tokens,
+                             const int64_t* targets, int64_t n_seq, int64_t T, const int32_t* member_seq,
+                             const int32_t* member_row, const float* member_sign, int64_t members, float* loss_sum,
+                             float* token_loss, float* logits, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- a7, a8, a9: fitness, gradient assembly, optimizer ---------------------------------------------------- */
+
+/* fitness[j] = (L[2j+1] - L[2j]) / (std + 1e-8) with the unbiased std over j < members / 2; weight[d] = sum of
+ * fitness[j] over j % pairs == d. fp32; members even.
+ * Replaces: archive/10M/train/val/eggroll.py:151-154. */
+int noise_fitness(const float* losses, int64_t members, int64_t pairs, float* fitness, float* weight, void* stream);
+
+/* grad[o, i] = scale * sum_j weight[j] a_j[o] b_j[i] over j < pairs, with a_j = rows[j * stride + a_off + (0..out)],
+ * b_j = rows[j * stride + b_off + (0..in)] (fp32 accumulation). 1-D parameters (b_off < 0):
+ * grad[i] = scale * sum_j weight[j] rows[j * stride + a_off + i] for i < in.
+ * Replaces: archive/10M/train/val/eggroll.py:155-166 (scale = -1 / len(fitness)). */
+int noise_outer_grad(const float* rows, int64_t stride, int64_t a_off, int64_t b_off, const float* weight,
+                     int64_t pairs, int64_t out, int64_t in, float scale, float* grad, void* stream);
+
+/* One AdamW step on n fp32 elements in place (torch.optim.AdamW arithmetic): p *= 1 - lr wd; m = lerp(m, g, 1-b1);
+ * v = b2 v + (1 - b2) g^2; p -= lr / (1 - b1^step) * m / (sqrt(v) / sqrt(1 - b2^step) + eps).
+ * shadow (optional): bf16 copy of the updated p. Replaces: archive/10M/train/val/eggroll.py:205, 167 and
+ * train/speedrun/run.py:2866-2883 (_adamw_kernel). */
+int noise_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                float eps, float weight_decay, int64_t step, uint16_t* shadow, void* stream);
+
+/* ---- a10, a11, a12: cross-token credit readout ------------------------------------------------------------ */
+
+/* lse[r, s] = log sum_{t in [s - window, s]} exp(q[r, s] . k[r, t] / 8); q, k bf16 [rows, T, 64], T % 64 == 0.
+ * Replaces: train/speedrun/moment_kernels.py:79-110, 137-164 (_implicit_key_statistics, its lse output). */
+int noise_credit_lse(const uint16_t* q, const uint16_t* k, int64_t rows, int64_t T, int32_t window, float* lse,
+                     void* stream);
+
+/* out[r, t, :] = sum_{s in [t, t + window]} exp(k[r, t] . q[r, s] / 8 - lse[r, s]) src[r, s, :]; src fp32
+ * [rows, T, 64] used as its bf16 high part (hi_lo != 0: high + low parts), probabilities in bf16, fp32 accumulation.
+ * Replaces: train/speedrun/moment_kernels.py:612-661 (_value_credit_kernel / _value_pass) and
+ * train/speedrun/value_gluon.py:145-172 (value_pass_gluon). */
+int noise_credit_value(const uint16_t* q, const uint16_t* k, const float* lse, const float* src, int64_t rows,
+                       int64_t T, int32_t window, int32_t hi_lo, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NOISE_AMD_H */

@@ -1,0 +1,68 @@
+// Shared definitions of the noise_amd HIP library (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/noise_amd.h"
+
+typedef uint16_t bf16_t;  // storage type of bfloat16 in global memory
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+// The fixed model's widths (utils/model.py:34-43, 69-79, 100-104).
+constexpr int kD = 512;       // n_embd
+constexpr int kH = 8;         // heads
+constexpr int kHD = 64;       // head_dim
+constexpr int kF = 2048;      // MLP hidden
+constexpr int kGateIn = 32;   // ve_gate input channels
+constexpr int kQKV = 3 * kD;  // fused q|k|v output width
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet), the rounding of torch's .to(torch.bfloat16).
+__host__ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u;
+#if defined(__HIP_DEVICE_COMPILE__)
+  u = __float_as_uint(f);
+#else
+  union { float f; uint32_t u; } c; c.f = f; u = c.u;
+#endif
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Error state of the C ABI (abi.cpp).
+int noise_set_error(int code, const char* fmt, ...);
+
+#define NOISE_CHECK_HIP(expr)                                                                   \
+  do {                                                                                          \
+    hipError_t _e = (expr);                                                                     \
+    if (_e != hipSuccess)                                                                       \
+      return noise_set_error(NOISE_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), \
+                             __FILE__, __LINE__);                                               \
+  } while (0)
+
+#define NOISE_REQUIRE(cond, ...)                                   \
+  do {                                                             \
+    if (!(cond)) return noise_set_error(NOISE_ERR_ARG, __VA_ARGS__); \
+  } while (0)
+
+#define NOISE_LAUNCH_CHECK() NOISE_CHECK_HIP(hipGetLastError())

@@ -1,0 +1,626 @@
+// The perturbed population forward of the fixed GPT (archive/10M/train/val/eggroll.py:66-103 over
+// utils/model.py:193-210), as row kernels + bf16 MFMA GEMMs with population epilogues + the windowed flash kernel.
+//
+// Rows: member i's token t is row r = i * T + t of every activation; all rows of a GEMM tile belong to one member
+// (T % 128 == 0), so a member's noise row, sign and rank-1 vectors are tile-uniform. The rank-1 correction
+// sign * (x . b) a^T of eggroll.py:56-58 is split between the producer of x, which writes x . b per row (or per-head /
+// per-tile partials of it), and the GEMM epilogue, which adds sign * (x . b) * a[col].
+#include <math.h>
+#include <string.h>
+
+#include "gemm.h"
+#include "window_flash.h"
+
+namespace noise {
+
+constexpr float kNormEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps, F.rms_norm's default
+
+struct Members {
+  int T;
+  const int32_t* seq;   // token row of each member
+  const int32_t* row;   // noise row of each member
+  const float* sign;    // +-sigma of each member
+  const float* noise;   // [n_rows, stride] or NULL (unperturbed)
+  int64_t stride;
+  const int64_t* tokens;   // [n_seq, T]
+  __device__ __forceinline__ int member(int64_t r) const { return (int)(r / T); }
+  __device__ __forceinline__ const float* nrow(int m) const { return noise ? noise + (int64_t)row[m] * stride : nullptr; }
+  __device__ __forceinline__ float sgn(int m) const { return noise ? sign[m] : 0.f; }
+  __device__ __forceinline__ int64_t token(int64_t r) const {
+    const int m = member(r);
+    return tokens[(int64_t)seq[m] * T + (r - (int64_t)m * T)];
+  }
+};
+
+// ---------------------------------------------------------------------------------------------------------------
+// x0 = norm(wte[tok] + sign a[tok] b)  (eggroll.py:61-63, 74); one wave per row, 8 channels per lane.
+__global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __restrict__ wte, int Vp, int64_t off_wte,
+                                                    float* __restrict__ x0, int64_t M) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= M) return;
+  const int lane = threadIdx.x & 63, c0 = lane * 8;
+  const int m = mb.member(r);
+  int64_t tok = mb.token(r);
+  const bool bad = tok < 0 || tok >= Vp;
+  if (bad) tok = 0;
+  const float* nr = mb.nrow(m);
+  const float s = mb.sgn(m);
+  const float at = nr ? s * nr[off_wte + tok] : 0.f;
+  float e[8], ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    e[j] = wte[tok * kD + c0 + j];
+    if (nr) e[j] += at * nr[off_wte + Vp + c0 + j];
+    ss += e[j] * e[j];
+  }
+  ss = warp_sum(ss);
+  const float inv = bad ? __builtin_nanf("") : rsqrtf(ss * (1.0f / kD) + kNormEps);
+  float* dst = x0 + r * kD + c0;
+  *(f32x4*)dst = f32x4{e[0] * inv, e[1] * inv, e[2] * inv, e[3] * inv};
+  *(f32x4*)(dst + 4) = f32x4{e[4] * inv, e[5] * inv, e[6] * inv, e[7] * inv};
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// [optional lambda mix] x = (l_r + s eps_r) x + (l_0 + s eps_0) x0 (eggroll.py:77-79), then h = norm(x) in bf16, the
+// dots h . b_k for up to 3 rank-1 vectors, and the value-embedding gate 2 sigmoid(h[:32] W_g^T + s (h[:32].b_g) a_g)
+// (eggroll.py:88). One wave per row.
+struct NormArgs {
+  float* x;             // [M, 512] fp32 (read; written back when mixing)
+  const float* x0;      // [M, 512] (mixing only)
+  int mix, first;       // first: x is taken to be x0
+  const float* resid_lambdas; const float* x0_lambdas; int layer;
+  int64_t off_resid, off_x0;
+  bf16_t* h;            // [M, 512]
+  int ndot; int64_t off_b[3];  // noise offsets of the b vectors
+  float* xb;            // [M, 4]
+  const float* w_gate;  // [8, 32] or NULL
+  int64_t off_gate;     // noise offset of ve_gate's (a[8] | b[32])
+  float* gate;          // [M, 8]
+  int64_t M;
+};
+
+__global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.M) return;
+  const int lane = threadIdx.x & 63, c0 = lane * 8;
+  const int m = mb.member(r);
+  const float* nr = mb.nrow(m);
+  const float s = mb.sgn(m);
+  float v[8];
+  const float* src = a.first ? a.x0 : a.x;
+  const f32x4 v0 = *(const f32x4*)(src + r * kD + c0), v1 = *(const f32x4*)(src + r * kD + c0 + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { v[j] = v0[j]; v[j + 4] = v1[j]; }
+  if (a.mix) {
+    float lr = a.resid_lambdas[a.layer], l0 = a.x0_lambdas[a.layer];
+    if (nr) { lr += s * nr[a.off_resid + a.layer]; l0 += s * nr[a.off_x0 + a.layer]; }
+    const f32x4 w0 = *(const f32x4*)(a.x0 + r * kD + c0), w1 = *(const f32x4*)(a.x0 + r * kD + c0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[j] = lr * v[j] + l0 * w0[j]; v[j + 4] = lr * v[j + 4] + l0 * w1[j]; }
+    float* dst = a.x + r * kD + c0;
+    *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+    *(f32x4*)(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+  ss = warp_sum(ss);
+  const float inv = rsqrtf(ss * (1.0f / kD) + kNormEps);
+  float hv[8];
+  bf16_t hb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) { hb[j] = f32_to_bf16(v[j] * inv); hv[j] = bf16_to_f32(hb[j]); }
+  u32x4 packed;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) packed[j] = (uint32_t)hb[2 * j] | ((uint32_t)hb[2 * j + 1] << 16);
+  *(u32x4*)(a.h + r * kD + c0) = packed;
+  if (nr) {
+    for (int k = 0; k < a.ndot; ++k) {
+      const float* bv = nr + a.off_b[k] + c0;
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d += hv[j] * bv[j];
+      d = warp_sum(d);
+      if (lane == 0) a.xb[r * 4 + k] = d;
+    }
+  }
+  if (a.w_gate) {
+    // channels 0..31 live in lanes 0..3
+    float g[kH], db = 0.f;
+#pragma unroll
+    for (int hd = 0; hd < kH; ++hd) {
+      float d = 0.f;
+      if (lane < 4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d += hv[j] * a.w_gate[hd * kGateIn + c0 + j];
+      }
+      g[hd] = d;
+    }
+    if (nr && lane < 4) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) db += hv[j] * nr[a.off_gate + kH + c0 + j];
+    }
+#pragma unroll
+    for (int hd = 0; hd < kH; ++hd) {
+      g[hd] += __shfl_xor(g[hd], 1, 64);
+      g[hd] += __shfl_xor(g[hd], 2, 64);
+    }
+    db += __shfl_xor(db, 1, 64);
+    db += __shfl_xor(db, 2, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int hd = 0; hd < kH; ++hd) {
+        float pre = g[hd];
+        if (nr) pre += s * db * nr[a.off_gate + hd];
+        a.gate[r * kH + hd] = 2.0f / (1.0f + expf(-pre));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// q, k = norm(rotary(q)), norm(rotary(k)) in place on the fused qkv rows (utils/model.py:55-58, 93-94). One wave per
+// row; a half-wave holds one head, lane j the rotary pair (j, j + 32).
+__global__ __launch_bounds__(256) void rope_norm_kernel(bf16_t* __restrict__ qkv, const float* __restrict__ cos_t,
+                                                        const float* __restrict__ sin_t, int T, int64_t M) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= M) return;
+  const int lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
+  const int t = (int)(r % T);
+  const float c = cos_t[t * 32 + j], s = sin_t[t * 32 + j];
+  bf16_t* row = qkv + r * kQKV;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int head = it * 2 + half;  // 0..15 over q (0..7) and k (8..15)
+    bf16_t* hp = row + head * kHD;
+    const float x1 = bf16_to_f32(hp[j]), x2 = bf16_to_f32(hp[j + 32]);
+    const float y1 = x1 * c + x2 * s, y2 = -x1 * s + x2 * c;
+    float ss = y1 * y1 + y2 * y2;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float inv = rsqrtf(ss * (1.0f / kHD) + kNormEps);
+    hp[j] = f32_to_bf16(y1 * inv);
+    hp[j + 32] = f32_to_bf16(y2 * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// out[r] = x[r, :K] . b_member (bf16 x, fp32 b); one wave per row.
+__global__ __launch_bounds__(256) void rowdot_kernel(Members mb, const bf16_t* __restrict__ x, int64_t ld, int K,
+                                                     int64_t off_b, float* __restrict__ out, int64_t M) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= M) return;
+  const int lane = threadIdx.x & 63;
+  const float* bv = mb.nrow(mb.member(r)) + off_b;
+  float d = 0.f;
+  for (int c0 = lane * 8; c0 < K; c0 += 512) {
+    const u32x4 p = *(const u32x4*)(x + r * ld + c0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      d += __uint_as_float(p[j] << 16) * bv[c0 + 2 * j] + __uint_as_float(p[j] & 0xFFFF0000u) * bv[c0 + 2 * j + 1];
+    }
+  }
+  d = warp_sum(d);
+  if (lane == 0) out[r] = d;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// GEMM epilogues
+
+// qkv = h W_qkv^T + s (h . b_seg) a_seg, plus gate * (ve[tok] + s a_ve[tok] b_ve) on the v columns.
+struct EpiQKV {
+  Members mb;
+  bf16_t* out;
+  int64_t off[3];   // noise offsets of c_q, c_k, c_v
+  const float* xb;  // [M, 4]
+  const float* gate;  // [M, 8] or NULL
+  const float* ve;    // [Vp, 512] or NULL
+  int64_t off_ve;
+  int Vp;
+  template <class S>
+  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*) const {
+    const int m = mb.member(row0);
+    const float* nr = mb.nrow(m);
+    const float s = mb.sgn(m);
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j) {
+      const int col = acc_col(col0, j, lane);
+      const int seg = col >> 9, c = col & (kD - 1);
+      const float av = nr ? s * nr[off[seg] + c] : 0.f;
+      const bool with_ve = (seg == 2) && ve;
+      const float bve = (with_ve && nr) ? nr[off_ve + Vp + c] : 0.f;
+#pragma unroll
+      for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = acc_row(row0, i, r, lane);
+          float v = acc[i][j][r];
+          if (nr) v += xb[row * 4 + seg] * av;
+          if (with_ve) {
+            int64_t tok = mb.token(row);
+            tok = (tok < 0 || tok >= Vp) ? 0 : tok;
+            float e = ve[tok * kD + c];
+            if (nr) e += s * nr[off_ve + tok] * bve;
+            v += gate[row * kH + (c >> 6)] * e;
+          }
+          out[row * kQKV + col] = f32_to_bf16(v);
+        }
+    }
+  }
+};
+
+// x[row, col] += acc + s (sum of xb partials) a[col]   (the residual adds of utils/model.py:118-119)
+struct EpiResid {
+  Members mb;
+  float* x;
+  int64_t ldx;
+  int64_t off;      // noise offset of the parameter's a
+  const float* xb;  // [M, nxb] partial dots, summed
+  int nxb;
+  template <class S>
+  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*) const {
+    const int m = mb.member(row0);
+    const float* nr = mb.nrow(m);
+    const float s = mb.sgn(m);
+    float xbv[S::TM][16];
+#pragma unroll
+    for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float d = 0.f;
+        if (nr) {
+          const int64_t row = acc_row(row0, i, r, lane);
+          for (int p = 0; p < nxb; ++p) d += xb[row * nxb + p];
+        }
+        xbv[i][r] = d;
+      }
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j) {
+      const int col = acc_col(col0, j, lane);
+      const float av = nr ? s * nr[off + col] : 0.f;
+#pragma unroll
+      for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = acc_row(row0, i, r, lane);
+          x[row * ldx + col] += acc[i][j][r] + xbv[i][r] * av;
+        }
+    }
+  }
+};
+
+// hidden = relu(acc + s (x . b) a)^2 in bf16 (utils/model.py:107)
+struct EpiReluSq {
+  Members mb;
+  bf16_t* out;
+  int64_t ldo;
+  int64_t off;
+  const float* xb;  // [M, xb_ld]: column 0 holds x . b
+  int xb_ld;
+  template <class S>
+  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*) const {
+    const int m = mb.member(row0);
+    const float* nr = mb.nrow(m);
+    const float s = mb.sgn(m);
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j) {
+      const int col = acc_col(col0, j, lane);
+      const float av = nr ? s * nr[off + col] : 0.f;
+#pragma unroll
+      for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = acc_row(row0, i, r, lane);
+          float v = acc[i][j][r];
+          if (nr) v += xb[row * xb_ld] * av;
+          v = fmaxf(v, 0.f);
+          out[row * ldo + col] = f32_to_bf16(v * v);
+        }
+    }
+  }
+};
+
+// logits z = 15 tanh((acc + s (h . b) a) / 15) (utils/model.py:203-204); per row of this workgroup's column tile the
+// partial max and sum of exp(z - max) over the first `vocab` columns, and the target's logit (utils/model.py:206-209).
+struct EpiHeadCE {
+  Members mb;
+  int64_t off;
+  const float* xb;    // [M, xb_ld]: column 0 holds h . b
+  int xb_ld;
+  int vocab, n_part;
+  float* part_max;    // [M, n_part]
+  float* part_sum;
+  float* tgt_logit;   // [M]
+  const int64_t* targets;  // [n_seq, T]
+  float* logits;      // [M, vocab] or NULL
+  template <class S>
+  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void* smem) const {
+    const int m = mb.member(row0);
+    const float* nr = mb.nrow(m);
+    const float s = mb.sgn(m);
+    float rowmax[S::TM][16];
+#pragma unroll
+    for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rowmax[i][r] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j) {
+      const int col = acc_col(col0, j, lane);
+      const float av = nr ? s * nr[off + col] : 0.f;
+#pragma unroll
+      for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = acc_row(row0, i, r, lane);
+          float z = acc[i][j][r];
+          if (nr) z += xb[row * xb_ld] * av;
+          // 15 tanh(z / 15) = 15 (1 - 2 / (exp(2 z / 15) + 1))
+          const float e2 = exp2f(z * (2.0f / 15.0f) * kLog2e);
+          z = 15.0f - 30.0f / (e2 + 1.0f);
+          if (col >= vocab) z = -INFINITY;
+          acc[i][j][r] = z;
+          rowmax[i][r] = fmaxf(rowmax[i][r], z);
+          if (col < vocab) {
+            if (logits) logits[row * vocab + col] = z;
+            const int t = (int)(row - (int64_t)m * mb.T);
+            const int64_t tg = targets[(int64_t)mb.seq[m] * mb.T + t];
+            if (tg == col) tgt_logit[row] = z;
+          }
+        }
+    }
+    // max over the 32 columns of a lane half, then sum of exp
+#pragma unroll
+    for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = rowmax[i][r];
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+        rowmax[i][r] = v;
+      }
+    float rowsum[S::TM][16];
+#pragma unroll
+    for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < S::TN; ++j) sum += exp2f((acc[i][j][r] - rowmax[i][r]) * kLog2e);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        rowsum[i][r] = sum;
+      }
+    // combine the WN waves of the workgroup through LDS: [WN][BM] (max, sum)
+    float* sm = (float*)smem;
+    const int wave = threadIdx.x >> 6, wn = wave % S::WN;
+    const int lrow0 = row0 - (int)(blockIdx.y * S::BM);
+    if ((lane & 31) == 0) {
+#pragma unroll
+      for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int lr = lrow0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+          sm[(wn * S::BM + lr) * 2] = rowmax[i][r];
+          sm[(wn * S::BM + lr) * 2 + 1] = rowsum[i][r];
+        }
+    }
+    __syncthreads();
+    for (int lr = threadIdx.x; lr < S::BM; lr += S::kThreads) {
+      float mx = -INFINITY;
+      for (int w = 0; w < S::WN; ++w) mx = fmaxf(mx, sm[(w * S::BM + lr) * 2]);
+      float sum = 0.f;
+      for (int w = 0; w < S::WN; ++w) {
+        const float wm = sm[(w * S::BM + lr) * 2];
+        if (wm > -INFINITY) sum += sm[(w * S::BM + lr) * 2 + 1] * exp2f((wm - mx) * kLog2e);
+      }
+      const int64_t row = (int64_t)blockIdx.y * S::BM + lr;
+      part_max[row * n_part + blockIdx.x] = mx;
+      part_sum[row * n_part + blockIdx.x] = sum;
+    }
+  }
+};
+
+// per-row CE from the column partials; a negative target contributes 0, an out-of-range one NaN.
+__global__ void ce_finalize_kernel(Members mb, const float* __restrict__ part_max, const float* __restrict__ part_sum,
+                                   int n_part, const float* __restrict__ tgt_logit, const int64_t* __restrict__ targets,
+                                   int vocab, float* __restrict__ row_ce, float* __restrict__ token_loss, int64_t M) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= M) return;
+  float mx = -INFINITY;
+  for (int p = 0; p < n_part; ++p) mx = fmaxf(mx, part_max[r * n_part + p]);
+  float sum = 0.f;
+  for (int p = 0; p < n_part; ++p) {
+    const float pm = part_max[r * n_part + p];
+    if (pm > -INFINITY) sum += part_sum[r * n_part + p] * expf(pm - mx);
+  }
+  const int m = mb.member(r);
+  const int64_t tg = targets[(int64_t)mb.seq[m] * mb.T + (r - (int64_t)m * mb.T)];
+  float ce;
+  if (tg < 0) ce = 0.f;
+  else if (tg >= vocab) ce = __builtin_nanf("");
+  else ce = mx + logf(sum) - tgt_logit[r];
+  row_ce[r] = ce;
+  if (token_loss) token_loss[r] = ce;
+}
+
+// loss_sum[m] = sum over the member's T rows, a fixed-order tree (deterministic).
+__global__ __launch_bounds__(256) void member_sum_kernel(const float* __restrict__ row_ce, int T, float* __restrict__ out) {
+  __shared__ float red[4];
+  const int m = blockIdx.x;
+  float s = 0.f;
+  for (int t = threadIdx.x; t < T; t += 256) s += row_ce[(int64_t)m * T + t];
+  s = warp_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[m] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+using Tile = GemmShape<128, 128, 64, 2, 2>;
+
+static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct Workspace {
+  float *x, *x0;
+  bf16_t *h, *qkv, *y, *hid;
+  float *xb, *gate, *xbp, *xb1, *pmax, *psum, *tgt, *row_ce;
+  size_t bytes;
+};
+
+static constexpr int kHeadParts = 4096 / Tile::BN;  // column tiles of the head GEMM at padded_vocab <= 4096
+
+static Workspace carve(void* base, int64_t M) {
+  Workspace w;
+  char* p = (char*)base;
+  size_t off = 0;
+  auto take = [&](size_t n) { char* q = p + off; off += align256(n); return (void*)q; };
+  w.x = (float*)take(M * kD * 4);
+  w.x0 = (float*)take(M * kD * 4);
+  w.h = (bf16_t*)take(M * kD * 2);
+  w.qkv = (bf16_t*)take(M * kQKV * 2);
+  w.y = (bf16_t*)take(M * kD * 2);
+  w.hid = (bf16_t*)take(M * kF * 2);
+  w.xb = (float*)take(M * 4 * 4);
+  w.gate = (float*)take(M * kH * 4);
+  w.xbp = (float*)take(M * kH * 4);
+  w.xb1 = (float*)take(M * 4);
+  w.pmax = (float*)take(M * kHeadParts * 4);
+  w.psum = (float*)take(M * kHeadParts * 4);
+  w.tgt = (float*)take(M * 4);
+  w.row_ce = (float*)take(M * 4);
+  w.bytes = off;
+  return w;
+}
+
+static bool g_prepared = false;
+static int prepare_all() {
+  if (g_prepared) return NOISE_OK;
+  NOISE_CHECK_HIP((prepare_gemm<Tile, EpiQKV>()));
+  NOISE_CHECK_HIP((prepare_gemm<Tile, EpiResid>()));
+  NOISE_CHECK_HIP((prepare_gemm<Tile, EpiReluSq>()));
+  NOISE_CHECK_HIP((prepare_gemm<Tile, EpiHeadCE>()));
+  g_prepared = true;
+  return NOISE_OK;
+}
+
+}  // namespace noise
+
+using namespace noise;
+
+extern "C" size_t noise_population_forward_workspace(int64_t members, int64_t T) {
+  if (members <= 0 || T <= 0) return 0;
+  return carve(nullptr, members * T).bytes;
+}
+
+extern "C" int noise_population_forward(const noise_gpt* model, const noise_perturbation* pert, const int64_t* tokens,
+                                        const int64_t* targets, int64_t n_seq, int64_t T, const int32_t* member_seq,
+                                        const int32_t* member_row, const float* member_sign, int64_t members,
+                                        float* loss_sum, float* token_loss, float* logits, void* workspace,
+                                        size_t workspace_bytes, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  NOISE_REQUIRE(model && pert, "model / perturbation is NULL");
+  NOISE_REQUIRE(members > 0 && n_seq > 0, "members and n_seq must be positive");
+  NOISE_REQUIRE(T > 0 && T % 128 == 0, "T = %lld must be a positive multiple of 128", (long long)T);
+  NOISE_REQUIRE(model->n_layer > 0 && model->n_layer <= NOISE_MAX_LAYERS, "n_layer %d outside [1, %d]", model->n_layer,
+                NOISE_MAX_LAYERS);
+  NOISE_REQUIRE(model->padded_vocab > 0 && model->padded_vocab % 128 == 0 && model->padded_vocab <= 4096,
+                "padded_vocab %d must be a multiple of 128 and <= 4096", model->padded_vocab);
+  NOISE_REQUIRE(model->vocab > 0 && model->vocab <= model->padded_vocab, "vocab %d outside [1, padded_vocab]",
+                model->vocab);
+  NOISE_REQUIRE(tokens && member_seq && member_row && member_sign, "tokens / member tables are NULL");
+  NOISE_REQUIRE(targets || logits, "need targets (losses) or logits");
+  NOISE_REQUIRE(model->wte && model->lm_head && model->rope_cos && model->rope_sin && model->resid_lambdas &&
+                    model->x0_lambdas, "model weight pointer is NULL");
+  const int64_t M = members * T;
+  NOISE_REQUIRE(M <= (int64_t)INT32_MAX / 4, "members * T = %lld too large", (long long)M);
+  Workspace ws = carve(workspace, M);
+  NOISE_REQUIRE(workspace && workspace_bytes >= ws.bytes, "workspace %zu bytes < %zu", workspace_bytes, ws.bytes);
+  int rc = prepare_all();
+  if (rc) return rc;
+
+  Members mb{(int)T, member_seq, member_row, member_sign, pert->rows, pert->stride, tokens};
+  const int Vp = model->padded_vocab;
+  const bool noisy = pert->rows != nullptr;
+  const unsigned row_blocks = (unsigned)((M + 3) / 4);
+
+  hipLaunchKernelGGL(embed_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte, ws.x0, M);
+  NOISE_LAUNCH_CHECK();
+
+  for (int i = 0; i < model->n_layer; ++i) {
+    const noise_layer& L = model->layers[i];
+    NOISE_REQUIRE(L.w_qkv && L.w_proj && L.w_fc && L.w_mlp_proj, "layer %d weight pointer is NULL", i);
+    NOISE_REQUIRE((L.w_gate == nullptr) == (L.ve == nullptr), "layer %d: w_gate and ve must both be set or both NULL", i);
+    NOISE_REQUIRE(L.window >= 0, "layer %d: negative window", i);
+    // lambda mix + norm + q/k/v dots + gate
+    NormArgs na;
+    memset(&na, 0, sizeof(na));
+    na.x = ws.x; na.x0 = ws.x0; na.mix = 1; na.first = (i == 0);
+    na.resid_lambdas = model->resid_lambdas; na.x0_lambdas = model->x0_lambdas; na.layer = i;
+    na.off_resid = pert->resid_lambdas; na.off_x0 = pert->x0_lambdas;
+    na.h = ws.h; na.ndot = 3;
+    na.off_b[0] = pert->c_q[i] + kD; na.off_b[1] = pert->c_k[i] + kD; na.off_b[2] = pert->c_v[i] + kD;
+    na.xb = ws.xb; na.w_gate = L.w_gate; na.off_gate = pert->ve_gate[i]; na.gate = ws.gate; na.M = M;
+    hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, na);
+    NOISE_LAUNCH_CHECK();
+
+    EpiQKV eq{mb, ws.qkv, {pert->c_q[i], pert->c_k[i], pert->c_v[i]}, ws.xb, L.w_gate ? ws.gate : nullptr, L.ve,
+              pert->ve[i], Vp};
+    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_qkv, kD, (int)M, kQKV, kD, eq, stream)));
+    hipLaunchKernelGGL(rope_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, ws.qkv, model->rope_cos,
+                       model->rope_sin, (int)T, M);
+    NOISE_LAUNCH_CHECK();
+
+    FlashArgs fa;
+    memset(&fa, 0, sizeof(fa));
+    fa.x = ws.qkv; fa.y = ws.qkv + kD; fa.v = ws.qkv + 2 * kD;
+    fa.x_sb = fa.y_sb = fa.v_sb = T * kQKV; fa.x_st = fa.y_st = fa.v_st = kQKV;
+    fa.out = ws.y; fa.o_sb = T * kD; fa.o_st = kD;
+    fa.xb_out = noisy ? ws.xbp : nullptr;
+    fa.xb_vec = noisy ? pert->rows + pert->c_proj[i] + kD : nullptr;
+    fa.xb_row = member_row; fa.xb_stride = pert->stride;
+    fa.heads = kH; fa.T = (int)T; fa.window = L.window;
+    hipLaunchKernelGGL(window_flash_kernel<kAttn>, dim3((unsigned)(T / kFlashBO), kH, (unsigned)members), dim3(256), 0,
+                       stream, fa);
+    NOISE_LAUNCH_CHECK();
+
+    EpiResid ep{mb, ws.x, kD, pert->c_proj[i], ws.xbp, kH};
+    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
+
+    NormArgs nb;
+    memset(&nb, 0, sizeof(nb));
+    nb.x = ws.x; nb.h = ws.h; nb.ndot = 1; nb.off_b[0] = pert->c_fc[i] + kF;  // c_fc's a spans its 2048 outputs
+    nb.xb = ws.xb; nb.M = M;
+    hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nb);
+    NOISE_LAUNCH_CHECK();
+
+    EpiReluSq er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4};
+    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
+    if (noisy) {
+      hipLaunchKernelGGL(rowdot_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, ws.hid, (int64_t)kF, kF,
+                         pert->mlp_proj[i] + kD, ws.xb1, M);
+      NOISE_LAUNCH_CHECK();
+    }
+    EpiResid em{mb, ws.x, kD, pert->mlp_proj[i], ws.xb1, 1};
+    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+  }
+
+  NormArgs nf;
+  memset(&nf, 0, sizeof(nf));
+  nf.x = ws.x; nf.h = ws.h; nf.ndot = 1; nf.off_b[0] = pert->lm_head + Vp; nf.xb = ws.xb; nf.M = M;
+  hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nf);
+  NOISE_LAUNCH_CHECK();
+
+  const int n_part = Vp / Tile::BN;
+  const int64_t* tg = targets ? targets : tokens;  // logits-only calls still run the CE bookkeeping on tokens
+  EpiHeadCE eh{mb, pert->lm_head, ws.xb, 4, model->vocab, n_part, ws.pmax, ws.psum, ws.tgt, tg, logits};
+  NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, model->lm_head, kD, (int)M, Vp, kD, eh, stream)));
+  if (targets && (loss_sum || token_loss)) {
+    hipLaunchKernelGGL(ce_finalize_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, stream, mb, ws.pmax,
+                       ws.psum, n_part, ws.tgt, targets, model->vocab, ws.row_ce, token_loss, M);
+    NOISE_LAUNCH_CHECK();
+    if (loss_sum) {
+      hipLaunchKernelGGL(member_sum_kernel, dim3((unsigned)members), dim3(256), 0, stream, ws.row_ce, (int)T, loss_sum);
+      NOISE_LAUNCH_CHECK();
+    }
+  }
+  return NOISE_OK;
+}

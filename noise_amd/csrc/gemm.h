@@ -1,0 +1,150 @@
+// bf16 MFMA GEMM for gfx950: C[M, N] = A[M, K] . B[N, K]^T with fp32 accumulation (both operands K-contiguous:
+// the x @ weight.t() of nn.Linear weights stored [out, in]). The accumulator tile goes to an epilogue functor, which
+// is where the population-specific work (rank-1 member corrections, residual adds, relu^2, soft-capped CE) happens.
+//
+// Tiling: a workgroup computes BM x BN with WM x WN waves; a wave owns (BM/WM) x (BN/WN) as 32x32 MFMA tiles
+// (v_mfma_f32_32x32x16_bf16). K advances in BK steps through two LDS buffers: the next tile's global loads are
+// issued before the current tile's MFMAs, and stored to the other buffer after them (one barrier per step).
+// LDS rows are BK bf16 = BK/8 16-byte chunks; chunk c of row r is stored at c ^ (r & 7), so the 8 rows a
+// ds_read_b128 phase touches fall on distinct banks.
+//
+// MFMA 32x32x16 bf16 lane layout (checked on gfx950): lane l supplies A[row l%32][k 8(l/32)..8(l/32)+7] and
+// B^T[col l%32][same k]; accumulator register r holds C[row (r/4)*8 + (l/32)*4 + r%4][col l%32].
+#pragma once
+
+#include "common.h"
+
+namespace noise {
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct GemmShape {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int kThreads = WM * WN * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
+  static constexpr int kChunks = BK / 8;              // 16-byte chunks per LDS row
+  static constexpr int kAVec = BM * kChunks / kThreads;  // 16-byte global loads per thread
+  static constexpr int kBVec = BN * kChunks / kThreads;
+  static constexpr int kLdsBytes = 2 * (BM + BN) * BK * 2;
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
+  static_assert(BK % 16 == 0 && kChunks <= 8 && kChunks >= 2, "BK in {16, 32, 64}");
+  static_assert((BM * kChunks) % kThreads == 0 && (BN * kChunks) % kThreads == 0, "tile loads must divide threads");
+};
+
+template <int kChunks>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return chunk ^ (row & (kChunks - 1));
+}
+
+// Row-major [rows x BK] bf16 tile of a K-contiguous matrix -> registers (16 bytes per vector).
+template <class S, int kVec>
+__device__ __forceinline__ void load_tile(const bf16_t* __restrict__ g, int64_t ld, int row0, int rows_valid, int k0,
+                                          u32x4 (&r)[kVec]) {
+#pragma unroll
+  for (int i = 0; i < kVec; ++i) {
+    const int v = threadIdx.x + i * S::kThreads;
+    const int row = v / S::kChunks, chunk = v % S::kChunks;
+    if (row < rows_valid)
+      r[i] = *(const u32x4*)(g + (int64_t)(row0 + row) * ld + k0 + chunk * 8);
+    else
+      r[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+template <class S, int kVec>
+__device__ __forceinline__ void store_tile(bf16_t* lds, const u32x4 (&r)[kVec]) {
+#pragma unroll
+  for (int i = 0; i < kVec; ++i) {
+    const int v = threadIdx.x + i * S::kThreads;
+    const int row = v / S::kChunks, chunk = v % S::kChunks;
+    *(u32x4*)(lds + row * S::BK + swz<S::kChunks>(row, chunk) * 8) = r[i];
+  }
+}
+
+template <class S>
+__device__ __forceinline__ bf16x8 read_frag(const bf16_t* lds, int row, int kchunk) {
+  return *(const bf16x8*)(lds + row * S::BK + swz<S::kChunks>(row, kchunk) * 8);
+}
+
+template <class S, class Epi>
+__global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __restrict__ A, int64_t lda,
+                                                              const bf16_t* __restrict__ B, int64_t ldb, int M, int N,
+                                                              int K, Epi epi) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16_t* lds = (bf16_t*)smem_raw;
+  bf16_t* As[2] = {lds, lds + S::BM * S::BK};
+  bf16_t* Bs[2] = {lds + 2 * S::BM * S::BK, lds + 2 * S::BM * S::BK + S::BN * S::BK};
+
+  const int m0 = blockIdx.y * S::BM, n0 = blockIdx.x * S::BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / S::WN, wn = wave % S::WN;
+  const int a_rows = min(S::BM, M - m0), b_rows = min(S::BN, N - n0);
+
+  f32x16 acc[S::TM][S::TN];
+#pragma unroll
+  for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  u32x4 ra[S::kAVec], rb[S::kBVec];
+  load_tile<S, S::kAVec>(A, lda, m0, a_rows, 0, ra);
+  load_tile<S, S::kBVec>(B, ldb, n0, b_rows, 0, rb);
+  store_tile<S, S::kAVec>(As[0], ra);
+  store_tile<S, S::kBVec>(Bs[0], rb);
+  __syncthreads();
+
+  const int nk = K / S::BK;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) {
+      load_tile<S, S::kAVec>(A, lda, m0, a_rows, (kt + 1) * S::BK, ra);
+      load_tile<S, S::kBVec>(B, ldb, n0, b_rows, (kt + 1) * S::BK, rb);
+    }
+    const bf16_t* as = As[cur];
+    const bf16_t* bs = Bs[cur];
+#pragma unroll
+    for (int kk = 0; kk < S::BK / 16; ++kk) {
+      bf16x8 fa[S::TM], fb[S::TN];
+#pragma unroll
+      for (int i = 0; i < S::TM; ++i) fa[i] = read_frag<S>(as, wm * S::WTM + i * 32 + (lane & 31), kk * 2 + (lane >> 5));
+#pragma unroll
+      for (int j = 0; j < S::TN; ++j) fb[j] = read_frag<S>(bs, wn * S::WTN + j * 32 + (lane & 31), kk * 2 + (lane >> 5));
+#pragma unroll
+      for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < S::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) {
+      store_tile<S, S::kAVec>(As[cur ^ 1], ra);
+      store_tile<S, S::kBVec>(Bs[cur ^ 1], rb);
+    }
+    __syncthreads();
+  }
+  epi.template apply<S>(acc, m0 + wm * S::WTM, n0 + wn * S::WTN, lane, (void*)smem_raw);
+}
+
+// Row / column of accumulator element (i, j, r) for this lane.
+__device__ __forceinline__ int acc_row(int row0, int i, int r, int lane) {
+  return row0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+}
+__device__ __forceinline__ int acc_col(int col0, int j, int lane) { return col0 + j * 32 + (lane & 31); }
+
+template <class S, class Epi>
+static inline hipError_t launch_gemm(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, int M, int N, int K,
+                                     const Epi& epi, hipStream_t stream) {
+  dim3 grid((N + S::BN - 1) / S::BN, (M + S::BM - 1) / S::BM);
+  hipLaunchKernelGGL((gemm_nt_kernel<S, Epi>), grid, dim3(S::kThreads), S::kLdsBytes, stream, A, lda, B, ldb, M, N,
+                     K, epi);
+  return hipGetLastError();
+}
+
+template <class S, class Epi>
+static inline hipError_t prepare_gemm() {
+  return hipFuncSetAttribute((const void*)gemm_nt_kernel<S, Epi>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             S::kLdsBytes);
+}
+
+}  // namespace noise

@@ -1,0 +1,137 @@
+// Counter-based noise kernels: the virtual Gaussian buffer, per-step offsets and per-direction noise rows.
+// Replaces archive/10M/train/val/eggroll.py:114 (buffer), :117-120 (offsets), :122-128 (noise slices).
+#include <string.h>
+
+#include "rng.h"
+
+namespace noise {
+
+constexpr int kMaxParams = 64;
+
+struct RowsArgs {
+  int32_t n_params;
+  int64_t width[kMaxParams];
+  int64_t col0[kMaxParams];   // column of the parameter's slice in a noise row
+  int64_t slot0[kMaxParams + 1];  // first thread slot of the parameter (width / 4 + 2 slots each)
+};
+
+// One thread per buffer quad overlapping [start, start + n).
+__global__ void buffer_kernel(uint64_t seed, uint64_t start, int64_t n, float* __restrict__ out) {
+  const uint64_t first = start >> 2;
+  const uint64_t blk = first + blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
+  const uint64_t last = (start + (uint64_t)n - 1) >> 2;
+  if (blk > last) return;
+  float z[4];
+  buffer_quad(seed, blk, z);
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint64_t i = 4 * blk + l;
+    if (i >= start && i < start + (uint64_t)n) out[i - start] = z[l];
+  }
+}
+
+__global__ void offsets_kernel(uint64_t seed, uint64_t step, RowsArgs args, int64_t pairs, int64_t* __restrict__ out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= (int64_t)args.n_params * pairs) return;
+  const int p = (int)(i / pairs);
+  const int64_t d = i - (int64_t)p * pairs;
+  const uint32_t range = (uint32_t)(kNoiseSize - (uint64_t)args.width[p]);
+  out[i] = offset_value(seed, step, (uint32_t)p, (uint32_t)d, range);
+}
+
+// grid.y walks the directions; x walks the quad slots of every parameter of the row.
+__global__ void rows_kernel(uint64_t seed, const int64_t* __restrict__ offsets, int64_t pairs, RowsArgs args,
+                            const int64_t* __restrict__ directions, int64_t n, int64_t stride, float* __restrict__ rows) {
+  const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (slot >= args.slot0[args.n_params]) return;
+  int p = 0;
+  while (p + 1 < args.n_params && slot >= args.slot0[p + 1]) ++p;
+  const int64_t width = args.width[p];
+  for (int64_t j = blockIdx.y; j < n; j += gridDim.y) {
+    const int64_t d = directions[j];
+    float* dst = rows + j * stride + args.col0[p];
+    if (d < 0 || d >= pairs) {  // an invalid direction poisons its row instead of reading out of bounds
+      const int64_t e0 = 4 * (slot - args.slot0[p]);
+      for (int64_t e = e0; e < e0 + 4 && e < width; ++e) dst[e] = __builtin_nanf("");
+      continue;
+    }
+    const uint64_t off = (uint64_t)offsets[(int64_t)p * pairs + d];
+    const uint64_t blk = (off >> 2) + (uint64_t)(slot - args.slot0[p]);
+    if (blk > ((off + (uint64_t)width - 1) >> 2)) continue;
+    float z[4];
+    buffer_quad(seed, blk, z);
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint64_t i = 4 * blk + l;
+      if (i >= off && i < off + (uint64_t)width) dst[i - off] = z[l];
+    }
+  }
+}
+
+static int make_rows_args(const int64_t* widths, int32_t n_params, RowsArgs* a) {
+  NOISE_REQUIRE(widths != nullptr, "widths is NULL");
+  NOISE_REQUIRE(n_params > 0 && n_params <= kMaxParams, "n_params %d outside [1, %d]", n_params, kMaxParams);
+  memset(a, 0, sizeof(*a));
+  a->n_params = n_params;
+  int64_t col = 0, slot = 0;
+  for (int p = 0; p < n_params; ++p) {
+    NOISE_REQUIRE(widths[p] > 0 && (uint64_t)widths[p] < kNoiseSize, "width[%d] = %lld outside (0, 2^28)", p,
+                  (long long)widths[p]);
+    a->width[p] = widths[p];
+    a->col0[p] = col;
+    a->slot0[p] = slot;
+    col += widths[p];
+    slot += widths[p] / 4 + 2;
+  }
+  a->slot0[n_params] = slot;
+  return NOISE_OK;
+}
+
+}  // namespace noise
+
+using namespace noise;
+
+extern "C" int noise_rng_buffer(uint64_t seed, uint64_t start, int64_t n, float* out, void* stream) {
+  NOISE_REQUIRE(n >= 0, "n < 0");
+  if (n == 0) return NOISE_OK;
+  NOISE_REQUIRE(out != nullptr, "out is NULL");
+  NOISE_REQUIRE(start + (uint64_t)n <= kNoiseSize, "buffer range [%llu, %llu) beyond 2^28", (unsigned long long)start,
+                (unsigned long long)(start + n));
+  const uint64_t quads = ((start + n - 1) >> 2) - (start >> 2) + 1;
+  const unsigned blocks = (unsigned)((quads + 255) / 256);
+  hipLaunchKernelGGL(buffer_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, seed, start, n, out);
+  NOISE_LAUNCH_CHECK();
+  return NOISE_OK;
+}
+
+extern "C" int noise_rng_offsets(uint64_t seed, uint64_t step, const int64_t* widths, int32_t n_params, int64_t pairs,
+                                 int64_t* out, void* stream) {
+  RowsArgs a;
+  int rc = make_rows_args(widths, n_params, &a);
+  if (rc) return rc;
+  NOISE_REQUIRE(pairs > 0 && pairs <= 0x7FFFFFFF, "pairs %lld outside [1, 2^31)", (long long)pairs);
+  NOISE_REQUIRE(out != nullptr, "out is NULL");
+  const int64_t total = (int64_t)n_params * pairs;
+  hipLaunchKernelGGL(offsets_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, seed,
+                     step, a, pairs, out);
+  NOISE_LAUNCH_CHECK();
+  return NOISE_OK;
+}
+
+extern "C" int noise_rng_rows(uint64_t seed, const int64_t* offsets, int64_t pairs, const int64_t* widths,
+                              int32_t n_params, const int64_t* directions, int64_t n, float* rows, void* stream) {
+  RowsArgs a;
+  int rc = make_rows_args(widths, n_params, &a);
+  if (rc) return rc;
+  NOISE_REQUIRE(pairs > 0, "pairs <= 0");
+  NOISE_REQUIRE(n >= 0, "n < 0");
+  if (n == 0) return NOISE_OK;
+  NOISE_REQUIRE(offsets && directions && rows, "NULL pointer argument");
+  const int64_t stride = a.col0[n_params - 1] + a.width[n_params - 1];
+  const unsigned bx = (unsigned)((a.slot0[n_params] + 255) / 256);
+  const unsigned by = (unsigned)(n < 65535 ? n : 65535);
+  hipLaunchKernelGGL(rows_kernel, dim3(bx, by), dim3(256), 0, (hipStream_t)stream, seed, offsets, pairs, a, directions,
+                     n, stride, rows);
+  NOISE_LAUNCH_CHECK();
+  return NOISE_OK;
+}

@@ -1,0 +1,245 @@
+"""The fixed GPT of Noise with the reference's host API (utils/model.py), whose forward runs on the MI355X kernels.
+
+GPTConfig, GPT(config, pad_vocab_size_to=64), init_weights(), forward(idx, targets=None, loss_reduction='mean') and
+the state-dict keys, shapes and order are those of utils/model.py:34-210, so a state dict moves between the two
+strictly (utils/eval.py:37-45). forward() calls the C-ABI population forward of libnoise_amd.so with one unperturbed
+member per sequence; there is no CPU path, and a CPU tensor or a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from . import _lib
+
+
+@dataclass
+class GPTConfig:
+    sequence_len: int = 2048
+    vocab_size: int = 4096
+    n_layer: int = 8
+    n_head: int = 8
+    n_kv_head: int = 8
+    n_embd: int = 512
+    # Per block, repeating: S = half-sequence window, L = full. The last block is always L.
+    window_pattern: str = 'SSSL'
+
+
+def norm(x):
+    return F.rms_norm(x, (x.size(-1),))
+
+
+def has_ve(layer_idx, n_layer):
+    """Value embeddings on every other block, counting back from the last (utils/model.py:50-52)."""
+    return layer_idx % 2 == (n_layer - 1) % 2
+
+
+def apply_rotary_emb(x, cos, sin):
+    d = x.shape[3] // 2
+    x1, x2 = x[..., :d], x[..., d:]
+    return torch.cat([x1 * cos + x2 * sin, x1 * -sin + x2 * cos], 3)
+
+
+def attention(q, k, v, window):
+    """Causal attention with a left window on [batch, token, head, 64] tensors (utils/model.py:24-31): the HIP
+    windowed flash kernel, bf16 operands, fp32 softmax statistics, bf16 output."""
+    _lib.require_device(q, k, v)
+    B, T, H, D = q.shape
+    if D != 64:
+        raise ValueError(f'head_dim must be 64, got {D}')
+    if T % 128:
+        raise ValueError(f'sequence length {T} must be a multiple of 128')
+    q, k, v = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    out = torch.empty_like(q)
+    _lib.call('noise_attention', _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), B, H, T, T * H * D, H * D, int(window),
+              _lib.ptr(out), T * H * D, H * D, None, _lib.stream(q.device))
+    return out
+
+
+class CausalSelfAttention(nn.Module):
+    def __init__(self, config, layer_idx):
+        super().__init__()
+        self.n_head = config.n_head
+        self.n_kv_head = config.n_kv_head
+        self.n_embd = config.n_embd
+        self.head_dim = self.n_embd // self.n_head
+        assert self.n_embd % self.n_head == 0
+        self.c_q = nn.Linear(self.n_embd, self.n_head * self.head_dim, bias=False)
+        self.c_k = nn.Linear(self.n_embd, self.n_kv_head * self.head_dim, bias=False)
+        self.c_v = nn.Linear(self.n_embd, self.n_kv_head * self.head_dim, bias=False)
+        self.c_proj = nn.Linear(self.n_embd, self.n_embd, bias=False)
+        self.ve_gate_channels = 32
+        self.ve_gate = (nn.Linear(self.ve_gate_channels, self.n_kv_head, bias=False)
+                        if has_ve(layer_idx, config.n_layer) else None)
+
+
+class MLP(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.c_fc = nn.Linear(config.n_embd, 4 * config.n_embd, bias=False)
+        self.c_proj = nn.Linear(4 * config.n_embd, config.n_embd, bias=False)
+
+
+class Block(nn.Module):
+    def __init__(self, config, layer_idx):
+        super().__init__()
+        self.attn = CausalSelfAttention(config, layer_idx)
+        self.mlp = MLP(config)
+
+
+class GPT(nn.Module):
+    def __init__(self, config, pad_vocab_size_to=64):
+        super().__init__()
+        self.config = config
+        self.window_sizes = self._compute_window_sizes(config)
+        padded_vocab = (config.vocab_size + pad_vocab_size_to - 1) // pad_vocab_size_to * pad_vocab_size_to
+        self.transformer = nn.ModuleDict({
+            'wte': nn.Embedding(padded_vocab, config.n_embd),
+            'h': nn.ModuleList([Block(config, i) for i in range(config.n_layer)]),
+        })
+        self.lm_head = nn.Linear(config.n_embd, padded_vocab, bias=False)
+        self.resid_lambdas = nn.Parameter(torch.ones(config.n_layer))
+        self.x0_lambdas = nn.Parameter(torch.zeros(config.n_layer))
+        head_dim = config.n_embd // config.n_head
+        kv_dim = config.n_kv_head * head_dim
+        self.value_embeds = nn.ModuleDict({
+            str(i): nn.Embedding(padded_vocab, kv_dim) for i in range(config.n_layer) if has_ve(i, config.n_layer)
+        })
+        self.rotary_seq_len = config.sequence_len * 10
+        cos, sin = self._precompute_rotary(self.rotary_seq_len, head_dim)
+        self.register_buffer('cos', cos, persistent=False)
+        self.register_buffer('sin', sin, persistent=False)
+        self._packed = None
+
+    @torch.no_grad()
+    def init_weights(self):
+        """utils/model.py:149-175: N(0,1) wte, N(0,1e-3) lm_head, U(+-sqrt(3/512)) q/k/v/c_fc/value embeddings,
+        zero c_proj and ve_gate, lambdas 1 and 0.1, bf16 rotary tables, bf16 embeddings on the GPU."""
+        torch.nn.init.normal_(self.transformer.wte.weight, mean=0.0, std=1.0)
+        torch.nn.init.normal_(self.lm_head.weight, mean=0.0, std=0.001)
+        s = 3 ** 0.5 * self.config.n_embd ** (-0.5)
+        for block in self.transformer.h:
+            torch.nn.init.uniform_(block.attn.c_q.weight, -s, s)
+            torch.nn.init.uniform_(block.attn.c_k.weight, -s, s)
+            torch.nn.init.uniform_(block.attn.c_v.weight, -s, s)
+            torch.nn.init.zeros_(block.attn.c_proj.weight)
+            torch.nn.init.uniform_(block.mlp.c_fc.weight, -s, s)
+            torch.nn.init.zeros_(block.mlp.c_proj.weight)
+        self.resid_lambdas.fill_(1.0)
+        self.x0_lambdas.fill_(0.1)
+        for ve in self.value_embeds.values():
+            torch.nn.init.uniform_(ve.weight, -s, s)
+        for block in self.transformer.h:
+            if block.attn.ve_gate is not None:
+                torch.nn.init.zeros_(block.attn.ve_gate.weight)
+        head_dim = self.config.n_embd // self.config.n_head
+        self.cos, self.sin = self._precompute_rotary(self.rotary_seq_len, head_dim)
+        if self.transformer.wte.weight.device.type == 'cuda':
+            self.transformer.wte.to(dtype=torch.bfloat16)
+            for ve in self.value_embeds.values():
+                ve.to(dtype=torch.bfloat16)
+        self._packed = None
+
+    def _precompute_rotary(self, seq_len, head_dim, base=10000):
+        device = self.transformer.wte.weight.device
+        inv_freq = 1.0 / base ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim)
+        t = torch.arange(seq_len, dtype=torch.float32, device=device)
+        freqs = torch.outer(t, inv_freq)
+        cos, sin = freqs.cos().bfloat16(), freqs.sin().bfloat16()
+        return cos[None, :, None, :], sin[None, :, None, :]
+
+    def _compute_window_sizes(self, config):
+        pattern = config.window_pattern.upper()
+        long_w, short_w = config.sequence_len, config.sequence_len // 2
+        char_to_w = {'L': (long_w, 0), 'S': (short_w, 0)}
+        sizes = [char_to_w[pattern[i % len(pattern)]] for i in range(config.n_layer)]
+        sizes[-1] = (long_w, 0)
+        return sizes
+
+    # ---- device views for the kernels -----------------------------------------------------------------------
+    def check_shape(self):
+        c = self.config
+        if (c.n_embd, c.n_head, c.n_kv_head) != (512, 8, 8):
+            raise ValueError('the HIP kernels are built for the fixed model: n_embd 512, 8 heads of 64')
+        if c.n_layer > _lib.MAX_LAYERS:
+            raise ValueError(f'n_layer {c.n_layer} > {_lib.MAX_LAYERS}')
+        if self.lm_head.weight.shape[0] % 128 or self.lm_head.weight.shape[0] > 4096:
+            raise ValueError('padded vocabulary must be a multiple of 128 and at most 4096')
+
+    def packed(self):
+        """bf16 GEMM operands, fp32 tables and the ctypes model struct; rebuilt when any parameter changed."""
+        params = list(self.parameters())
+        key = tuple((p.data_ptr(), p._version) for p in params)
+        if self._packed is not None and self._packed[0] == key:
+            return self._packed[1]
+        self.check_shape()
+        dev = self.lm_head.weight.device
+        _lib.require_device(self.lm_head.weight)
+        keep = {}
+        bf = lambda t: t.detach().to(torch.bfloat16).contiguous()
+        f32 = lambda t: t.detach().to(torch.float32).contiguous()
+        s = _lib.NoiseGpt()
+        s.n_layer = self.config.n_layer
+        s.vocab = self.config.vocab_size
+        s.padded_vocab = self.lm_head.weight.shape[0]
+        keep['resid'] = f32(self.resid_lambdas)
+        keep['x0l'] = f32(self.x0_lambdas)
+        keep['wte'] = f32(self.transformer.wte.weight)
+        keep['lm_head'] = bf(self.lm_head.weight)
+        s.resid_lambdas, s.x0_lambdas = keep['resid'].data_ptr(), keep['x0l'].data_ptr()
+        s.wte, s.lm_head = keep['wte'].data_ptr(), keep['lm_head'].data_ptr()
+        for i, block in enumerate(self.transformer.h):
+            a, m = block.attn, block.mlp
+            L = s.layers[i]
+            keep[f'qkv{i}'] = bf(torch.cat([a.c_q.weight, a.c_k.weight, a.c_v.weight]))
+            keep[f'proj{i}'] = bf(a.c_proj.weight)
+            keep[f'fc{i}'] = bf(m.c_fc.weight)
+            keep[f'mproj{i}'] = bf(m.c_proj.weight)
+            L.w_qkv, L.w_proj = keep[f'qkv{i}'].data_ptr(), keep[f'proj{i}'].data_ptr()
+            L.w_fc, L.w_mlp_proj = keep[f'fc{i}'].data_ptr(), keep[f'mproj{i}'].data_ptr()
+            if a.ve_gate is not None:
+                keep[f'gate{i}'] = f32(a.ve_gate.weight)
+                keep[f've{i}'] = f32(self.value_embeds[str(i)].weight)
+                L.w_gate, L.ve = keep[f'gate{i}'].data_ptr(), keep[f've{i}'].data_ptr()
+            L.window = int(self.window_sizes[i][0])
+        self._packed = (key, (s, keep, dev))
+        return self._packed[1]
+
+    def rope_tables(self, T):
+        cos = self.cos[0, :T, 0, :].float().contiguous()
+        sin = self.sin[0, :T, 0, :].float().contiguous()
+        return cos, sin
+
+    def forward(self, idx, targets=None, loss_reduction='mean'):
+        """utils/model.py:193-210 on the HIP kernels: logits fp32 [B, T, vocab] (soft-capped) without targets,
+        otherwise the cross-entropy ('mean' over targets != -1, 'sum', or 'none' [B * T])."""
+        _lib.require_device(idx)
+        B, T = idx.shape
+        Tp = (T + 127) // 128 * 128
+        idx = idx.to(torch.int64)
+        if Tp != T:  # causal: trailing padding does not reach the real positions
+            idx = F.pad(idx, (0, Tp - T))
+        tg = None
+        if targets is not None:
+            tg = targets.to(torch.int64)
+            if Tp != T:
+                tg = F.pad(tg, (0, Tp - T), value=-1)
+            tg = tg.contiguous()
+        from .population import run_forward
+        out = run_forward(self, idx.contiguous(), tg, member_seq=torch.arange(B, device=idx.device, dtype=torch.int32),
+                          noise=None, want_logits=targets is None, want_tokens=loss_reduction == 'none')
+        if targets is None:
+            return out['logits'].view(B, Tp, -1)[:, :T]
+        if loss_reduction == 'none':
+            return out['token_loss'].view(B, Tp)[:, :T].reshape(-1)
+        total = out['loss_sum'].sum()
+        if loss_reduction == 'sum':
+            return total
+        if loss_reduction == 'mean':
+            return total / (targets != -1).sum()
+        raise ValueError(f'unknown loss_reduction {loss_reduction!r}')

@@ -1,0 +1,262 @@
+"""EGGROLL's population training step on the MI355X kernels, with the reference's host API
+(archive/10M/train/val/eggroll.py): lowrank, lowrank_embed, population_loss and Eggroll(model, pairs, rank, world)
+with offsets(step), noise(offsets, directions) and step(x, y, optimizer, step).
+
+A direction's noise is a set of contiguous slices of one virtual N(0,1) buffer of 2^28 values at per-step offsets
+(eggroll.py:107-128); here the buffer is a counter-based generator (Philox4x32-10 + Box-Muller) evaluated on the GPU,
+so nothing of 1 GiB is ever stored. All of a direction's slices sit side by side in one noise row, in
+named_parameters() order; the forward kernels read a member's a and b vectors from its row.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+NOISE = 2 ** 28
+SEED = 0
+SIGMA = 0.002
+CHUNK = 256
+
+
+class NoiseLayout:
+    """Columns of every parameter's (a | b) slice (eps for 1-D parameters) in a noise row."""
+
+    def __init__(self, model):
+        self.names, self.shapes, self.widths, self.col0 = [], [], [], []
+        col = 0
+        for name, p in model.named_parameters():
+            w = int(sum(p.shape))
+            self.names.append(name)
+            self.shapes.append(tuple(p.shape))
+            self.widths.append(w)
+            self.col0.append(col)
+            col += w
+        self.stride = col
+        self.index = {n: i for i, n in enumerate(self.names)}
+        self.widths_c = (ctypes.c_int64 * len(self.widths))(*self.widths)
+
+    def col(self, name):
+        return self.col0[self.index[name]]
+
+    def struct(self, rows, n_layer):
+        s = _lib.NoisePerturbation()
+        s.rows = None if rows is None else rows.data_ptr()
+        s.stride = self.stride
+        s.resid_lambdas, s.x0_lambdas = self.col('resid_lambdas'), self.col('x0_lambdas')
+        s.wte, s.lm_head = self.col('transformer.wte.weight'), self.col('lm_head.weight')
+        for i in range(n_layer):
+            pre = f'transformer.h.{i}.'
+            s.c_q[i] = self.col(pre + 'attn.c_q.weight')
+            s.c_k[i] = self.col(pre + 'attn.c_k.weight')
+            s.c_v[i] = self.col(pre + 'attn.c_v.weight')
+            s.c_proj[i] = self.col(pre + 'attn.c_proj.weight')
+            s.c_fc[i] = self.col(pre + 'mlp.c_fc.weight')
+            s.mlp_proj[i] = self.col(pre + 'mlp.c_proj.weight')
+            if pre + 'attn.ve_gate.weight' in self.index:
+                s.ve_gate[i] = self.col(pre + 'attn.ve_gate.weight')
+                s.ve[i] = self.col(f'value_embeds.{i}.weight')
+        return s
+
+
+_WORKSPACE = {}
+
+
+def workspace(device, nbytes):
+    """One cached device workspace per device, grown on demand (the kernels themselves never allocate)."""
+    buf = _WORKSPACE.get(device)
+    if buf is None or buf.numel() < nbytes:
+        _WORKSPACE.pop(device, None)
+        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _WORKSPACE[device] = buf
+    return buf
+
+
+def run_forward(model, tokens, targets, member_seq, noise=None, member_row=None, member_sign=None, layout=None,
+                want_logits=False, want_tokens=False, want_sum=True):
+    """One call of noise_population_forward: members evaluate rows of tokens [n_seq, T] (T % 128 == 0).
+
+    noise: fp32 rows [n_rows, layout.stride] or None; member_row / member_sign: int32 / fp32 [members]."""
+    s, keep, dev = model.packed()
+    n_seq, T = tokens.shape
+    members = member_seq.numel()
+    cos, sin = model.rope_tables(T)
+    s.rope_cos, s.rope_sin = cos.data_ptr(), sin.data_ptr()
+    layout = layout or NoiseLayout(model)
+    if noise is None:
+        member_row = torch.zeros(members, dtype=torch.int32, device=dev)
+        member_sign = torch.zeros(members, dtype=torch.float32, device=dev)
+    pert = layout.struct(noise, model.config.n_layer)
+    out = {}
+    out['loss_sum'] = torch.empty(members, dtype=torch.float32, device=dev) if (targets is not None and want_sum) else None
+    out['token_loss'] = torch.empty(members * T, dtype=torch.float32, device=dev) if want_tokens else None
+    out['logits'] = (torch.empty(members * T, model.config.vocab_size, dtype=torch.float32, device=dev)
+                     if want_logits else None)
+    nbytes = _lib.lib().noise_population_forward_workspace(members, T)
+    ws = workspace(dev, nbytes)
+    _lib.call('noise_population_forward', ctypes.byref(s), ctypes.byref(pert), _lib.ptr(tokens), _lib.ptr(targets),
+              n_seq, T, _lib.ptr(member_seq), _lib.ptr(member_row), _lib.ptr(member_sign), members,
+              _lib.ptr(out['loss_sum']), _lib.ptr(out['token_loss']), _lib.ptr(out['logits']), _lib.ptr(ws),
+              ws.numel(), _lib.stream(dev))
+    return out
+
+
+def lowrank(x, weight, a, b, sign):
+    """x [m, T, in] through W [out, in] + sign a b^T, one (a [m, out], b [m, in], sign [m]) per member
+    (eggroll.py:56-58), as one grouped bf16 MFMA GEMM with the rank-1 term in its epilogue; fp32 [m, T, out]."""
+    _lib.require_device(x, weight, a, b, sign)
+    m, T, n_in = x.shape
+    n_out = weight.shape[0]
+    xb = x.to(torch.bfloat16).contiguous()
+    wb = weight.to(torch.bfloat16).contiguous()
+    rows = torch.cat([a.float(), b.float()], 1).contiguous()
+    sg = sign.float().contiguous()
+    y = torch.empty(m, T, n_out, dtype=torch.float32, device=x.device)
+    ws = workspace(x.device, _lib.lib().noise_lowrank_workspace(m, T, n_in, n_out, 0))
+    _lib.call('noise_lowrank', _lib.ptr(xb), 0, _lib.ptr(wb), _lib.ptr(rows), rows.shape[1], 0, n_out, _lib.ptr(sg),
+              m, T, n_in, n_out, _lib.ptr(y), None, _lib.ptr(ws), ws.numel(), _lib.stream(x.device))
+    return y
+
+
+def lowrank_sumsq(x, weight, rows, a_off, b_off, sign, shared=True):
+    """Per-member sum of squares of x W^T + sign (x . b) a^T with x shared by every member (the single perturbed
+    linear of BASELINE config 2); a / b are read from fp32 noise rows [m, stride] at a_off / b_off."""
+    m = sign.numel()
+    T, n_in = x.shape[-2], x.shape[-1]
+    n_out = weight.shape[0]
+    out = torch.empty(m, dtype=torch.float32, device=x.device)
+    ws = workspace(x.device, _lib.lib().noise_lowrank_workspace(m, T, n_in, n_out, int(shared)))
+    _lib.call('noise_lowrank', _lib.ptr(x), int(shared), _lib.ptr(weight), _lib.ptr(rows), rows.shape[1], a_off, b_off,
+              _lib.ptr(sign), m, T, n_in, n_out, None, _lib.ptr(out), _lib.ptr(ws), ws.numel(), _lib.stream(x.device))
+    return out
+
+
+def lowrank_embed(weight, a, b, idx, sign):
+    """Embedding rows of W [V, d] + sign a b^T for token ids idx [T] (eggroll.py:61-63)."""
+    return weight[idx].unsqueeze(0) + sign[:, None, None] * a[:, idx].unsqueeze(-1) * b[:, None, :]
+
+
+def pack_noise(layout, noise, m, device):
+    """name -> (a, b) / eps per-member tensors (the reference's noise dict) -> one fp32 row per member."""
+    parts = []
+    for name, shape in zip(layout.names, layout.shapes):
+        v = noise[name]
+        parts.append(torch.cat([v[0], v[1]], 1) if isinstance(v, tuple) else v)
+    return torch.cat([p.to(device=device, dtype=torch.float32) for p in parts], 1).contiguous()
+
+
+def population_loss(model, p, noise, sign, idx, targets):
+    """Mean cross-entropy [m] of m perturbed models on one sequence (eggroll.py:66-103). p is accepted for the
+    reference's signature; the model's own parameters are used. noise: name -> (a [m, out], b [m, in]) or eps [m, L]."""
+    del p
+    dev = model.lm_head.weight.device
+    layout = NoiseLayout(model)
+    m, T = sign.shape[0], idx.shape[0]
+    rows = pack_noise(layout, noise, m, dev)
+    Tp = (T + 127) // 128 * 128
+    tok = torch.nn.functional.pad(idx.to(torch.int64), (0, Tp - T)).view(1, Tp).contiguous()
+    tg = torch.nn.functional.pad(targets.to(torch.int64), (0, Tp - T), value=-1).view(1, Tp).contiguous()
+    out = run_forward(model, tok, tg, member_seq=torch.zeros(m, dtype=torch.int32, device=dev), noise=rows,
+                      member_row=torch.arange(m, dtype=torch.int32, device=dev),
+                      member_sign=sign.to(device=dev, dtype=torch.float32).contiguous(), layout=layout)
+    return out['loss_sum'] / T
+
+
+class Eggroll:
+    """Perturbation bookkeeping of eggroll.py:106-168 on the GPU: per-step offsets from a counter-based generator,
+    noise rows generated in place, the population forward in chunks of 2 * chunk members, fitness, the outer-product
+    gradient assembly and the optimizer step."""
+
+    def __init__(self, model, pairs, rank=0, world=1, sigma=SIGMA, seed=SEED, chunk=CHUNK):
+        self.model, self.pairs, self.rank, self.world = model, pairs, rank, world
+        self.sigma, self.seed, self.chunk = sigma, seed, chunk
+        self.device = next(model.parameters()).device
+        self.params = dict(model.named_parameters())
+        self.layout = NoiseLayout(model)
+        self.last = {}
+
+    def offsets(self, step):
+        """name -> int64 [pairs] offsets for this step (eggroll.py:117-120)."""
+        table = self.offset_table(step)
+        return {name: table[i] for i, name in enumerate(self.layout.names)}
+
+    def offset_table(self, step):
+        out = torch.empty(len(self.layout.names), self.pairs, dtype=torch.int64, device=self.device)
+        _lib.call('noise_rng_offsets', self.seed, step, self.layout.widths_c, len(self.layout.names), self.pairs,
+                  _lib.ptr(out), _lib.stream(self.device))
+        return out
+
+    def rows(self, table, directions):
+        """fp32 noise rows [n, stride] of the given directions."""
+        directions = directions.to(device=self.device, dtype=torch.int64).contiguous()
+        rows = torch.empty(directions.numel(), self.layout.stride, dtype=torch.float32, device=self.device)
+        _lib.call('noise_rng_rows', self.seed, _lib.ptr(table), self.pairs, self.layout.widths_c,
+                  len(self.layout.names), _lib.ptr(directions), directions.numel(), _lib.ptr(rows),
+                  _lib.stream(self.device))
+        return rows
+
+    def noise(self, offsets, directions):
+        """name -> (a [n, out], b [n, in]) for matrices and embeddings, eps [n, L] for 1-D (eggroll.py:122-128)."""
+        table = torch.stack([offsets[n] for n in self.layout.names]).contiguous()
+        rows = self.rows(table, directions)
+        out = {}
+        for name, shape, c0, w in zip(self.layout.names, self.layout.shapes, self.layout.col0, self.layout.widths):
+            sl = rows[:, c0:c0 + w]
+            out[name] = (sl[:, :shape[0]], sl[:, shape[0]:]) if len(shape) == 2 else sl
+        return out
+
+    def member_layout(self, n_seq):
+        members = max(2 * self.pairs, 2 * n_seq)
+        per_seq, per_rank = members // n_seq, members // self.world
+        if per_rank % (2 * self.chunk):
+            raise ValueError('each rank must evaluate whole chunks of pairs')
+        g = torch.arange(self.rank * per_rank, (self.rank + 1) * per_rank, device=self.device)
+        start = g - g % (2 * self.chunk)
+        return members, (g // 2) % self.pairs, torch.where(g % 2 == 0, 1.0, -1.0), start // per_seq
+
+    @torch.no_grad()
+    def step(self, x, y, optimizer, step):
+        """Evaluate this rank's share of the population, gather the losses, rebuild the update everywhere
+        (eggroll.py:130-168). Returns the mean population loss (a host sync)."""
+        n_seq, T = x.shape
+        if T % 128:
+            raise ValueError(f'sequence length {T} must be a multiple of 128')
+        members, direction, sgn, seq = self.member_layout(n_seq)
+        table = self.offset_table(step)
+        rows = self.rows(table, torch.arange(self.pairs, device=self.device))
+        tokens, targets = x.to(torch.int64).contiguous(), y.to(torch.int64).contiguous()
+        per_rank = direction.numel()
+        losses = torch.empty(per_rank, dtype=torch.float32, device=self.device)
+        m_chunk = 2 * self.chunk
+        for c in range(0, per_rank, m_chunk):
+            sl = slice(c, c + m_chunk)
+            out = run_forward(self.model, tokens, targets, member_seq=seq[sl].to(torch.int32).contiguous(),
+                              noise=rows, member_row=direction[sl].to(torch.int32).contiguous(),
+                              member_sign=(sgn[sl] * self.sigma).float().contiguous(), layout=self.layout)
+            losses[sl] = out['loss_sum'] / T
+        if self.world > 1:
+            gathered = [torch.empty_like(losses) for _ in range(self.world)]
+            torch.distributed.all_gather(gathered, losses)
+            losses = torch.cat(gathered)
+        n_fit = losses.numel() // 2
+        fitness = torch.empty(n_fit, dtype=torch.float32, device=self.device)
+        weight = torch.empty(self.pairs, dtype=torch.float32, device=self.device)
+        _lib.call('noise_fitness', _lib.ptr(losses), losses.numel(), self.pairs, _lib.ptr(fitness), _lib.ptr(weight),
+                  _lib.stream(self.device))
+        optimizer.zero_grad(set_to_none=True)
+        for name, shape, c0 in zip(self.layout.names, self.layout.shapes, self.layout.col0):
+            p = self.params[name]
+            grad = torch.empty(shape, dtype=torch.float32, device=self.device)
+            if len(shape) == 2:
+                _lib.call('noise_outer_grad', _lib.ptr(rows), self.layout.stride, c0, c0 + shape[0], _lib.ptr(weight),
+                          self.pairs, shape[0], shape[1], -1.0 / n_fit, _lib.ptr(grad), _lib.stream(self.device))
+            else:
+                _lib.call('noise_outer_grad', _lib.ptr(rows), self.layout.stride, c0, -1, _lib.ptr(weight),
+                          self.pairs, 1, shape[0], -1.0 / n_fit, _lib.ptr(grad), _lib.stream(self.device))
+            p.grad = grad.to(p.dtype)
+        optimizer.step()
+        self.last = dict(losses=losses, fitness=fitness, weight=weight)
+        return losses.mean().item()

@@ -1,0 +1,216 @@
+"""ORACLE — test infrastructure only (imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg;
+never by the product package noise_amd).
+
+Eager fp32 CPU restatement of the fixed GPT's forward and of EGGROLL's population forward, in plain torch ops on
+CPU tensors, written from the reference's semantics:
+
+  utils/model.py:46-47     norm            F.rms_norm over the last axis, eps = finfo(float32).eps
+  utils/model.py:50-52     has_ve          value embeddings on blocks with i % 2 == (L - 1) % 2
+  utils/model.py:55-58     apply_rotary    halves (x1, x2): (x1 cos + x2 sin, -x1 sin + x2 cos)
+  utils/model.py:17-31     attention       causal, left window: query s sees keys s - W .. s, scale 1/sqrt(64)
+  utils/model.py:81-97     attention block q/k/v, 2 sigmoid(ve_gate(h[:32])) value embedding, rotary, QK norm
+  utils/model.py:100-107   MLP             c_proj(relu(c_fc(x))^2)
+  utils/model.py:116-120   Block           pre-norm residual
+  utils/model.py:123-147   parameters      named_parameters order (a module's own parameters, then its children's)
+  utils/model.py:177-183   rotary tables   base 10000, cos/sin rounded to bfloat16
+  utils/model.py:185-191   windows         'SSSL' with S = T/2, L = T, last block L
+  utils/model.py:193-210   forward         norm(wte) -> blocks with lambda mix -> norm -> lm_head -> 15 tanh(z/15) -> CE
+  archive/10M/train/val/eggroll.py:56-58   lowrank         x W^T + sign (x b) a^T
+  archive/10M/train/val/eggroll.py:61-63   lowrank_embed   W[idx] + sign a[:, idx] b
+  archive/10M/train/val/eggroll.py:66-103  population_loss per-member CE of m perturbed models on one sequence
+
+Arithmetic is fp32 throughout (the reference runs the same graph under bf16 autocast; the GPU path is compared to
+this oracle within the stated tolerances). Parity pins: tests/test_oracle_model.py (closed forms at init, textbook
+causal SDPA when windows cover the sequence, brute-force materialized W + sigma a b^T, and the golden fixtures
+written from the reference's own functions in tests/golden/).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+FP32_EPS = torch.finfo(torch.float32).eps
+
+
+@dataclass
+class Config:
+    """GPTConfig defaults (utils/model.py:34-43)."""
+    sequence_len: int = 2048
+    vocab_size: int = 4096
+    n_layer: int = 8
+    n_head: int = 8
+    n_kv_head: int = 8
+    n_embd: int = 512
+    window_pattern: str = 'SSSL'
+
+    @property
+    def head_dim(self):
+        return self.n_embd // self.n_head
+
+    @property
+    def padded_vocab(self):
+        return (self.vocab_size + 63) // 64 * 64
+
+
+def has_ve(i, n_layer):
+    return i % 2 == (n_layer - 1) % 2
+
+
+def param_specs(cfg: Config):
+    """(name, shape) of every parameter in named_parameters() order (utils/model.py:123-147, 61-79, 100-104)."""
+    L, d, V = cfg.n_layer, cfg.n_embd, cfg.padded_vocab
+    kv = cfg.n_kv_head * cfg.head_dim
+    specs = [('resid_lambdas', (L,)), ('x0_lambdas', (L,)), ('transformer.wte.weight', (V, d))]
+    for i in range(L):
+        pre = f'transformer.h.{i}.'
+        specs += [(pre + 'attn.c_q.weight', (cfg.n_head * cfg.head_dim, d)), (pre + 'attn.c_k.weight', (kv, d)),
+                  (pre + 'attn.c_v.weight', (kv, d)), (pre + 'attn.c_proj.weight', (d, d))]
+        if has_ve(i, L):
+            specs.append((pre + 'attn.ve_gate.weight', (cfg.n_kv_head, 32)))
+        specs += [(pre + 'mlp.c_fc.weight', (4 * d, d)), (pre + 'mlp.c_proj.weight', (d, 4 * d))]
+    specs.append(('lm_head.weight', (V, d)))
+    specs += [(f'value_embeds.{i}.weight', (V, kv)) for i in range(L) if has_ve(i, L)]
+    return specs
+
+
+def window_sizes(cfg: Config):
+    long_w, short_w = cfg.sequence_len, cfg.sequence_len // 2
+    pattern = cfg.window_pattern.upper()
+    sizes = [long_w if pattern[i % len(pattern)] == 'L' else short_w for i in range(cfg.n_layer)]
+    sizes[-1] = long_w
+    return sizes
+
+
+def rms_norm(x):
+    return x * torch.rsqrt(x.square().mean(-1, keepdim=True) + FP32_EPS)
+
+
+def rotary(T, head_dim, base=10000.0):
+    """cos, sin [T, head_dim/2] as fp32 values of the reference's bfloat16 tables."""
+    inv_freq = 1.0 / base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim)
+    freqs = torch.outer(torch.arange(T, dtype=torch.float32), inv_freq)
+    return freqs.cos().bfloat16().float(), freqs.sin().bfloat16().float()
+
+
+def apply_rotary(x, cos, sin):
+    """x [..., T, H, D]; cos, sin [T, D/2]."""
+    d = x.shape[-1] // 2
+    c, s = cos[:, None, :], sin[:, None, :]
+    x1, x2 = x[..., :d], x[..., d:]
+    return torch.cat([x1 * c + x2 * s, x1 * -s + x2 * c], -1)
+
+
+def attention(q, k, v, window):
+    """q, k, v [B, T, H, D] -> [B, T, H, D]; query s sees keys t with 0 <= s - t <= window."""
+    T = q.shape[1]
+    pos = torch.arange(T)
+    lag = pos[:, None] - pos[None, :]
+    allowed = (lag >= 0) & (lag <= window)
+    qh, kh, vh = (z.transpose(1, 2) for z in (q, k, v))
+    logits = (qh @ kh.transpose(-1, -2)) / math.sqrt(q.shape[-1])
+    p = logits.masked_fill(~allowed, float('-inf')).softmax(-1)
+    return (p @ vh).transpose(1, 2)
+
+
+def softcap_ce(logits, targets):
+    """Per-token CE of 15 tanh(z / 15) logits (utils/model.py:203-209), ignore_index -1 -> 0 loss."""
+    z = 15.0 * torch.tanh(logits / 15.0)
+    lse = torch.logsumexp(z, -1)
+    t = targets.clamp(min=0)
+    picked = z.gather(-1, t.unsqueeze(-1)).squeeze(-1)
+    return torch.where(targets >= 0, lse - picked, torch.zeros_like(lse))
+
+
+def gpt_forward(p, cfg: Config, idx, targets=None, reduction='mean'):
+    """GPT.forward (utils/model.py:193-210) with parameters p: name -> fp32 CPU tensor."""
+    B, T = idx.shape
+    H, D = cfg.n_head, cfg.head_dim
+    cos, sin = rotary(T, D)
+    windows = window_sizes(cfg)
+    x = x0 = rms_norm(p['transformer.wte.weight'][idx])
+    for i in range(cfg.n_layer):
+        pre = f'transformer.h.{i}.'
+        x = p['resid_lambdas'][i] * x + p['x0_lambdas'][i] * x0
+        h = rms_norm(x)
+        q = (h @ p[pre + 'attn.c_q.weight'].t()).view(B, T, H, D)
+        k = (h @ p[pre + 'attn.c_k.weight'].t()).view(B, T, H, D)
+        v = (h @ p[pre + 'attn.c_v.weight'].t()).view(B, T, H, D)
+        if has_ve(i, cfg.n_layer):
+            ve = p[f'value_embeds.{i}.weight'][idx].view(B, T, H, D)
+            gate = 2 * torch.sigmoid(h[..., :32] @ p[pre + 'attn.ve_gate.weight'].t())
+            v = v + gate.unsqueeze(-1) * ve
+        q, k = rms_norm(apply_rotary(q, cos, sin)), rms_norm(apply_rotary(k, cos, sin))
+        y = attention(q, k, v, windows[i]).reshape(B, T, -1)
+        x = x + y @ p[pre + 'attn.c_proj.weight'].t()
+        hidden = torch.relu(rms_norm(x) @ p[pre + 'mlp.c_fc.weight'].t()).square()
+        x = x + hidden @ p[pre + 'mlp.c_proj.weight'].t()
+    logits = (rms_norm(x) @ p['lm_head.weight'].t())[..., :cfg.vocab_size]
+    if targets is None:
+        return 15.0 * torch.tanh(logits / 15.0)
+    ce = softcap_ce(logits, targets)
+    if reduction == 'none':
+        return ce.reshape(-1)
+    if reduction == 'sum':
+        return ce.sum()
+    return ce.sum() / (targets >= 0).sum()
+
+
+def lowrank(x, weight, a, b, sign):
+    """x [m, T, in] through W [out, in] + sign a b^T (eggroll.py:56-58)."""
+    return x @ weight.t() + sign[:, None, None] * (x @ b.unsqueeze(-1)) * a[:, None, :]
+
+
+def lowrank_embed(weight, a, b, idx, sign):
+    """W[idx] + sign a[:, idx] b (eggroll.py:61-63); idx [T]."""
+    return weight[idx].unsqueeze(0) + sign[:, None, None] * a[:, idx].unsqueeze(-1) * b[:, None, :]
+
+
+def population_loss(p, cfg: Config, noise, sign, idx, targets):
+    """Per-member summed CE [m] (eggroll.py:66-103 returns the mean: divide by the token count).
+
+    noise: name -> (a [m, out], b [m, in]) for matrices and embeddings, eps [m, L] for the lambdas; sign [m];
+    idx, targets [T]."""
+    H, D = cfg.n_head, cfg.head_dim
+    m, T = sign.shape[0], idx.shape[0]
+    cos, sin = rotary(T, D)
+    windows = window_sizes(cfg)
+    s = sign[:, None, None]
+    x = x0 = rms_norm(lowrank_embed(p['transformer.wte.weight'], *noise['transformer.wte.weight'], idx, sign))
+    for i in range(cfg.n_layer):
+        pre = f'transformer.h.{i}.'
+        resid = p['resid_lambdas'][i] + s * noise['resid_lambdas'][:, i, None, None]
+        mix = p['x0_lambdas'][i] + s * noise['x0_lambdas'][:, i, None, None]
+        x = resid * x + mix * x0
+        lin = lambda name, inp: lowrank(inp, p[pre + name], *noise[pre + name], sign)
+        h = rms_norm(x)
+        q = lin('attn.c_q.weight', h).view(m, T, H, D)
+        k = lin('attn.c_k.weight', h).view(m, T, H, D)
+        v = lin('attn.c_v.weight', h).view(m, T, H, D)
+        if has_ve(i, cfg.n_layer):
+            name = f'value_embeds.{i}.weight'
+            ve = lowrank_embed(p[name], *noise[name], idx, sign).view(m, T, H, D)
+            gate = 2 * torch.sigmoid(lin('attn.ve_gate.weight', h[..., :32]))
+            v = v + gate.unsqueeze(-1) * ve
+        q, k = rms_norm(apply_rotary(q, cos, sin)), rms_norm(apply_rotary(k, cos, sin))
+        y = attention(q, k, v, windows[i]).reshape(m, T, -1)
+        x = x + lin('attn.c_proj.weight', y)
+        x = x + lin('mlp.c_proj.weight', torch.relu(lin('mlp.c_fc.weight', rms_norm(x))).square())
+    h = rms_norm(x)
+    a, b = noise['lm_head.weight']
+    logits = lowrank(h, p['lm_head.weight'], a, b, sign)[..., :cfg.vocab_size]
+    return softcap_ce(logits, targets.unsqueeze(0).expand(m, T)).sum(-1)
+
+
+def flops_per_member_token(cfg: Config, T=None):
+    """Algorithmic forward FLOPs per member-token: 2 x matmul params + in-window causal attention (QK^T and PV)."""
+    T = T or cfg.sequence_len
+    d, L = cfg.n_embd, cfg.n_layer
+    mat = L * (4 * d * d + 2 * 4 * d * d) + sum(cfg.n_kv_head * 32 for i in range(L) if has_ve(i, L)) \
+        + cfg.padded_vocab * d
+    att = 0.0
+    for w in window_sizes(cfg):
+        keys = sum(min(t, w) + 1 for t in range(T)) / T
+        att += 4 * d * keys
+    return 2 * mat + att

@@ -1,0 +1,95 @@
+"""ORACLE — test infrastructure only. ctypes view of oracle/rng.c (the C restatement of the counter-based noise) and
+an independent vectorised numpy Philox4x32-10 used to cross-check it.
+
+Reference semantics restated (noise buffer, per-step offsets, direction slices): archive/10M/train/val/eggroll.py:35,
+114, 117-128. The generator itself is this build's definition; rng.c's header gives it in full.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / '_build' / 'liboracle.so'
+NOISE = 2 ** 28
+
+_lib = None
+
+
+def lib():
+    """The oracle's C library, built with oracle/Makefile on first use if it is missing."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            subprocess.run(['make', '-s', '-C', str(HERE)], check=True)
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _lib.oracle_philox4x32_10.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 3
+        _lib.oracle_ln.argtypes = [ctypes.c_float]
+        _lib.oracle_ln.restype = ctypes.c_float
+        _lib.oracle_sincos2pi.argtypes = [ctypes.c_float, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
+        _lib.oracle_noise_buffer.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int64, ctypes.c_void_p]
+        _lib.oracle_noise_offsets.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                                              ctypes.c_int64, ctypes.c_void_p]
+        _lib.oracle_noise_rows.argtypes = [ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                           ctypes.c_void_p]
+    return _lib
+
+
+def philox(ctr, key):
+    c = (ctypes.c_uint32 * 4)(*ctr)
+    k = (ctypes.c_uint32 * 2)(*key)
+    out = (ctypes.c_uint32 * 4)()
+    lib().oracle_philox4x32_10(c, k, out)
+    return tuple(out)
+
+
+def ln(u):
+    return lib().oracle_ln(u)
+
+
+def sincos2pi(u):
+    s, c = ctypes.c_float(), ctypes.c_float()
+    lib().oracle_sincos2pi(u, ctypes.byref(s), ctypes.byref(c))
+    return s.value, c.value
+
+
+def buffer(seed, start, n):
+    out = np.empty(n, np.float32)
+    lib().oracle_noise_buffer(seed, start, n, out.ctypes.data)
+    return out
+
+
+def offsets(seed, step, param, width, n):
+    """off_p[d], d < n, for a parameter whose direction spans `width` = sum(shape) values."""
+    out = np.empty(n, np.int64)
+    lib().oracle_noise_offsets(seed, step, param, NOISE - width, n, out.ctypes.data)
+    return out
+
+
+def rows(seed, offs, width):
+    offs = np.ascontiguousarray(offs, np.int64)
+    out = np.empty((len(offs), width), np.float32)
+    lib().oracle_noise_rows(seed, offs.ctypes.data, len(offs), width, out.ctypes.data)
+    return out
+
+
+def philox_numpy(c0, c1, c2, c3, k0, k1):
+    """Vectorised Philox4x32-10 over uint32 arrays (independent restatement of the SC'11 round function)."""
+    M0, M1 = np.uint64(0xD2511F53), np.uint64(0xCD9E8D57)
+    W0, W1 = np.uint32(0x9E3779B9), np.uint32(0xBB67AE85)
+    c = [np.asarray(x, np.uint32).copy() for x in (c0, c1, c2, c3)]
+    k0, k1 = np.uint32(k0), np.uint32(k1)
+    mask = np.uint64(0xFFFFFFFF)
+    for _ in range(10):
+        p0 = M0 * c[0].astype(np.uint64)
+        p1 = M1 * c[2].astype(np.uint64)
+        hi0, lo0 = (p0 >> np.uint64(32)).astype(np.uint32), (p0 & mask).astype(np.uint32)
+        hi1, lo1 = (p1 >> np.uint64(32)).astype(np.uint32), (p1 & mask).astype(np.uint32)
+        c = [hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0]
+        k0 = np.uint32((int(k0) + int(W0)) & 0xFFFFFFFF)
+        k1 = np.uint32((int(k1) + int(W1)) & 0xFFFFFFFF)
+    return c

@@ -1,0 +1,85 @@
+"""GPU parity of the credit readout (rows a10-a12) and the attention forward (a5) against the oracle.
+
+Tolerances: credit outputs within 2e-2 max relative error (max |gpu - ref| / max |ref|, the bound BASELINE.json
+states), lse within 2e-2 absolute (bf16 operands; logits up to 8 in magnitude)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import credit as oc
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+
+
+def _qk(rows, T, unit_rms, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(rows, T, 64, generator=g)
+    k = torch.randn(rows, T, 64, generator=g)
+    if unit_rms:  # the reference feeds RMS-normed q/k (train/val/run.py:975-976): logits up to +-8
+        q, k = om.rms_norm(q), om.rms_norm(k)
+    else:
+        q, k = q / 8, k / 8
+    return q.bfloat16(), k.bfloat16()
+
+
+def _relmax(got, ref):
+    return (got - ref).abs().max().item() / ref.abs().max().item()
+
+
+@pytest.mark.parametrize('T,window,unit', [(256, 256, True), (256, 64, True), (384, 128, False), (128, 0, True)])
+def test_lse_and_value_pass(dev, T, window, unit):
+    from noise_amd import credit
+    print(f'credit T={T} window={window} unit={unit}', flush=True)
+    rows = 3
+    q, k = _qk(rows, T, unit, seed=T + window)
+    src = torch.randn(rows, T, 64, generator=torch.Generator().manual_seed(1))
+    lse_ref = oc.lse(q.float(), k.float(), window)
+    lse = credit.credit_lse(q.to(dev), k.to(dev), window).cpu()
+    assert (lse - lse_ref).abs().max().item() < 2e-2
+    out_ref = oc.value_pass(q.float(), k.float(), lse_ref, src, window)
+    for hi_lo in (False, True):
+        out = credit.raw_value_credits(q.to(dev), k.to(dev), lse.to(dev), src.to(dev), window, hi_lo=hi_lo).cpu()
+        assert _relmax(out, out_ref) < 2e-2, (hi_lo, _relmax(out, out_ref))
+    # the dense eager definition (Boost.attention_maps + value_credit) end to end
+    full = credit.value_credit(q.to(dev), k.to(dev), src.to(dev), window).cpu()
+    dense = oc.credit_dense(q.float(), k.float(), src, window)
+    assert _relmax(full, dense) < 2e-2
+
+
+def test_credit_conservation_c3_shape(dev):
+    """Config 3 at full size: sum_t credit_t = sum_s e_s (every row of the softmax sums to 1)."""
+    from noise_amd import credit
+    print('credit conservation B16 H8 T2048', flush=True)
+    rows, T = 16 * 8, 2048
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = (torch.randn(rows, T, 64, device=dev, generator=g) / 8).bfloat16()
+    k = (torch.randn(rows, T, 64, device=dev, generator=g) / 8).bfloat16()
+    e = torch.randn(rows, T, 64, device=dev, generator=g)
+    for window in (T, 1024):
+        out = credit.value_credit(q, k, e, window, hi_lo=True)
+        lhs, rhs = out.double().sum(1), e.double().sum(1)
+        rel = ((lhs - rhs).abs().max() / rhs.abs().max()).item()
+        assert rel < 2e-2, (window, rel)
+
+
+def test_credit_q0_closed_form(dev):
+    from noise_amd import credit
+    T, W = 256, 100
+    q = torch.zeros(2, T, 64, dtype=torch.bfloat16)
+    k = torch.randn(2, T, 64).bfloat16()
+    e = torch.randn(2, T, 64)
+    out = credit.value_credit(q.to(dev), k.to(dev), e.to(dev), W, hi_lo=True).cpu()
+    ref = oc.credit_q0_closed_form(e, W)
+    assert _relmax(out, ref) < 1e-2
+
+
+@pytest.mark.parametrize('T,window', [(256, 256), (256, 128), (384, 100)])
+def test_attention_forward(dev, T, window):
+    from noise_amd.model import attention
+    print(f'attention T={T} window={window}', flush=True)
+    g = torch.Generator().manual_seed(T * 7 + window)
+    q, k, v = (om.rms_norm(torch.randn(2, T, 8, 64, generator=g)) for _ in range(3))
+    ref = om.attention(q.bfloat16().float(), k.bfloat16().float(), v.bfloat16().float(), window)
+    out = attention(q.to(dev), k.to(dev), v.to(dev), window).float().cpu()
+    assert _relmax(out, ref) < 2e-2

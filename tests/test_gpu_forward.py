@@ -1,0 +1,110 @@
+"""GPU parity of the fixed GPT's forward and of the population forward (rows a2-a6) against the fp32 oracle.
+
+Tolerance: per-token / per-member losses within 1e-2 relative (bf16 operands, fp32 accumulation), the bound
+BASELINE.json states for per-member losses."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from tests.golden import recipe
+
+pytestmark = pytest.mark.gpu
+
+SEQ = 256  # windows 128 (S) and 256 (L) at sequence_len 256
+
+
+def _cfgs():
+    ocfg = om.Config(sequence_len=SEQ)
+    from noise_amd.model import GPTConfig
+    return ocfg, GPTConfig(sequence_len=SEQ)
+
+
+_W = {}
+
+
+def _weights(ocfg):
+    if SEQ not in _W:
+        _W[SEQ] = recipe.weights(ocfg, seed=99)
+    return _W[SEQ]
+
+
+def _model(dev, w, gcfg):
+    from noise_amd.model import GPT
+    with torch.device('meta'):
+        model = GPT(gcfg)
+    model.to_empty(device=dev)
+    model.init_weights()
+    model.transformer.wte.float()
+    for e in model.value_embeds.values():
+        e.float()
+    model.load_state_dict({k: v.to(dev) for k, v in w.items()}, strict=True)
+    return model
+
+
+def test_gpt_forward_matches_oracle(dev):
+    print('gpt forward B=2 T=256', flush=True)
+    ocfg, gcfg = _cfgs()
+    w = _weights(ocfg)
+    model = _model(dev, w, gcfg)
+    idx, tg = recipe.tokens(ocfg, batch=2, ignore_every=37)
+    ref = om.gpt_forward(w, ocfg, idx, tg, 'none')
+    got = model(idx.to(dev), tg.to(dev), loss_reduction='none').cpu()
+    mask = tg.reshape(-1) >= 0
+    rel = ((got - ref).abs()[mask] / ref[mask].abs()).max().item()
+    assert rel < 1e-2, rel
+    assert torch.all(got[~mask] == 0)
+    s = model(idx.to(dev), tg.to(dev), loss_reduction='sum').item()
+    assert abs(s - ref.sum().item()) / ref.sum().item() < 1e-2
+    mean = model(idx.to(dev), tg.to(dev)).item()
+    assert abs(mean - ref.sum().item() / mask.sum().item()) / mean < 1e-2
+    logits = model(idx.to(dev)).cpu()
+    lref = om.gpt_forward(w, ocfg, idx)
+    assert ((logits - lref).abs().max() / lref.abs().max()).item() < 2e-2
+
+
+def test_gpt_forward_short_sequence_padding(dev):
+    """T = 100 (not a multiple of 128) is padded on the right; causal attention keeps the real positions exact."""
+    ocfg, gcfg = _cfgs()
+    w = _weights(ocfg)
+    model = _model(dev, w, gcfg)
+    idx, tg = recipe.tokens(ocfg, batch=1)
+    idx, tg = idx[:, :100], tg[:, :100]
+    ref = om.gpt_forward(w, ocfg, idx, tg, 'none')
+    got = model(idx.to(dev), tg.to(dev), loss_reduction='none').cpu()
+    assert got.shape == ref.shape
+    assert ((got - ref).abs() / ref.abs()).max().item() < 1e-2
+
+
+def test_population_loss_matches_oracle(dev):
+    from noise_amd.population import population_loss
+    print('population loss m=16 T=256', flush=True)
+    ocfg, gcfg = _cfgs()
+    w = _weights(ocfg)
+    model = _model(dev, w, gcfg)
+    members, sigma = 16, 0.05
+    noise = recipe.population_noise(ocfg, members, seed=77, step=2)
+    sign = torch.tensor([sigma, -sigma] * (members // 2))
+    idx, tg = recipe.tokens(ocfg, batch=1, seed=31)
+    ref = om.population_loss(w, ocfg, noise, sign, idx[0], tg[0]) / SEQ
+    dnoise = {k: tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for k, v in noise.items()}
+    got = population_loss(model, None, dnoise, sign.to(dev), idx[0].to(dev), tg[0].to(dev)).cpu()
+    rel = ((got - ref).abs() / ref.abs()).max().item()
+    assert rel < 1e-2, (got, ref)
+    # the antithetic differences (the fitness signal) follow the oracle's: correlation over the 8 pairs
+    d_ref, d_got = (ref[1::2] - ref[0::2]).numpy(), (got[1::2] - got[0::2]).numpy()
+    assert np.corrcoef(d_ref, d_got)[0, 1] > 0.9, (d_ref, d_got)
+
+
+def test_lowrank_matches_bruteforce(dev):
+    """x (W + s a b^T)^T with the perturbed weight materialized, on the CPU."""
+    from noise_amd.population import lowrank
+    g = torch.Generator().manual_seed(5)
+    m, T, n_in, n_out = 3, 128, 512, 256
+    x = torch.randn(m, T, n_in, generator=g).bfloat16().float()
+    W = (torch.randn(n_out, n_in, generator=g) * 0.05).bfloat16().float()
+    a, b = torch.randn(m, n_out, generator=g), torch.randn(m, n_in, generator=g)
+    sign = torch.tensor([0.01, -0.01, 0.02])
+    ref = torch.stack([x[i] @ (W + sign[i] * torch.outer(a[i], b[i])).t() for i in range(m)])
+    got = lowrank(x.to(dev), W.to(dev), a.to(dev), b.to(dev), sign.to(dev)).cpu()
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < 1e-2

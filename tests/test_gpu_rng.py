@@ -1,0 +1,53 @@
+"""GPU parity of the counter-based noise (row a1): values, offsets and rows bit-exact against the oracle's C
+restatement (oracle/rng.c)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import rng as orng
+from oracle.eggroll import step_offsets
+from oracle.model import Config, param_specs
+
+pytestmark = pytest.mark.gpu
+
+
+def test_buffer_bit_exact(dev):
+    from noise_amd import _lib
+    for start, n in [(0, 4096), (1, 1023), (3, 5), ((1 << 28) - 777, 777), (123456789, 70001)]:
+        print(f'buffer start={start} n={n}', flush=True)
+        out = torch.empty(n, dtype=torch.float32, device=dev)
+        _lib.call('noise_rng_buffer', 0, start, n, _lib.ptr(out), _lib.stream(dev))
+        ref = orng.buffer(0, start, n)
+        got = out.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (start, n, np.abs(got - ref).max())
+
+
+def test_buffer_other_seed(dev):
+    from noise_amd import _lib
+    out = torch.empty(1 << 16, dtype=torch.float32, device=dev)
+    _lib.call('noise_rng_buffer', 0xDEADBEEF12345, 999, 1 << 16, _lib.ptr(out), _lib.stream(dev))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orng.buffer(0xDEADBEEF12345, 999, 1 << 16).view(np.uint32))
+
+
+def test_offsets_and_rows_bit_exact(dev):
+    from noise_amd.model import GPT, GPTConfig
+    from noise_amd.population import Eggroll
+    cfg = Config()
+    with torch.device('meta'):
+        model = GPT(GPTConfig())
+    model.to_empty(device=dev)
+    pairs = 37
+    es = Eggroll(model, pairs, seed=5)
+    table = es.offset_table(step=11)
+    ref = step_offsets(cfg, 5, 11, pairs)
+    for p, (name, shape) in enumerate(param_specs(cfg)):
+        assert np.array_equal(table[p].cpu().numpy(), ref[name]), name
+    dirs = torch.tensor([0, 36, 5, 5, 17], device=dev)
+    rows = es.rows(table, dirs).cpu().numpy()
+    c0 = 0
+    for p, (name, shape) in enumerate(param_specs(cfg)):
+        w = int(sum(shape))
+        want = orng.rows(5, ref[name][dirs.cpu().numpy()], w)
+        assert np.array_equal(rows[:, c0:c0 + w].view(np.uint32), want.view(np.uint32)), name
+        c0 += w
+    assert c0 == rows.shape[1] == 101552

@@ -1,0 +1,101 @@
+"""GPU parity of the EGGROLL update (rows a7-a9) and of a whole Eggroll.step against the oracle.
+
+Tolerances: fitness and AdamW fp32 (1e-5 relative); gradients assembled in fp32 from the same noise (1e-4 relative);
+per-member losses 1e-2 relative (bf16 forward)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import eggroll as oe
+from oracle import model as om
+from tests.golden import recipe
+
+pytestmark = pytest.mark.gpu
+
+
+def test_fitness(dev):
+    from noise_amd import _lib
+    r = np.random.default_rng(0)
+    for members, pairs in [(64, 32), (24576, 12288), (48, 8)]:
+        L = torch.from_numpy(r.normal(8.3, 0.05, members).astype(np.float32))
+        f = torch.empty(members // 2, device=dev)
+        w = torch.empty(pairs, device=dev)
+        _lib.call('noise_fitness', _lib.ptr(L.to(dev)), members, pairs, _lib.ptr(f), _lib.ptr(w), _lib.stream(dev))
+        fr = oe.fitness(L)
+        wr = oe.direction_weights(fr, pairs)
+        assert torch.allclose(f.cpu(), fr, rtol=1e-4, atol=1e-4)
+        assert torch.allclose(w.cpu(), wr, rtol=1e-4, atol=1e-4)
+
+
+def test_outer_grad_and_vector_grad(dev):
+    from noise_amd import _lib
+    g = torch.Generator().manual_seed(1)
+    pairs, out, n_in, stride = 300, 130, 70, 260
+    rows = torch.randn(pairs, stride, generator=g)
+    w = torch.randn(pairs, generator=g)
+    grad = torch.empty(out, n_in, device=dev)
+    _lib.call('noise_outer_grad', _lib.ptr(rows.to(dev)), stride, 5, 5 + out, _lib.ptr(w.to(dev)), pairs, out, n_in,
+              -0.25, _lib.ptr(grad), _lib.stream(dev))
+    want = -0.25 * (w[:, None] * rows[:, 5:5 + out]).t().double() @ rows[:, 5 + out:5 + out + n_in].double()
+    assert torch.allclose(grad.cpu().double(), want, rtol=1e-4, atol=1e-4)
+    vec = torch.empty(8, device=dev)
+    _lib.call('noise_outer_grad', _lib.ptr(rows.to(dev)), stride, 3, -1, _lib.ptr(w.to(dev)), pairs, 1, 8, 2.0,
+              _lib.ptr(vec), _lib.stream(dev))
+    assert torch.allclose(vec.cpu(), 2.0 * (w @ rows[:, 3:11]), rtol=1e-4, atol=1e-4)
+
+
+def test_adamw_matches_torch(dev):
+    from noise_amd.optim import AdamW
+    g = torch.Generator().manual_seed(2)
+    p0 = torch.randn(5000, generator=g)
+    ref = torch.nn.Parameter(p0.clone())
+    mine = torch.nn.Parameter(p0.clone().to(dev))
+    opt_ref = torch.optim.AdamW([ref], lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    opt = AdamW([mine], lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    for _ in range(4):
+        grad = torch.randn(5000, generator=g)
+        ref.grad, mine.grad = grad.clone(), grad.to(dev)
+        opt_ref.step()
+        opt.step()
+    assert torch.allclose(mine.detach().cpu(), ref.detach(), rtol=1e-5, atol=1e-7)
+
+
+def test_eggroll_step_decomposed(dev):
+    """One Eggroll.step on a 256-token model: losses vs the oracle's population forward, fitness from those losses,
+    and the gradient the oracle assembles from the GPU's own direction weights."""
+    from noise_amd.model import GPT, GPTConfig
+    from noise_amd.population import Eggroll
+    ocfg = om.Config(sequence_len=256)
+    w = recipe.weights(ocfg, seed=99)
+    with torch.device('meta'):
+        model = GPT(GPTConfig(sequence_len=256))
+    model.to_empty(device=dev)
+    model.init_weights()
+    model.transformer.wte.float()
+    for e in model.value_embeds.values():
+        e.float()
+    model.load_state_dict({k: v.to(dev) for k, v in w.items()}, strict=True)
+    model.requires_grad_(False)
+    pairs, sigma, seed, step = 8, 0.05, 3, 1
+    es = Eggroll(model, pairs, sigma=sigma, seed=seed, chunk=4)
+    idx, tg = recipe.tokens(ocfg, batch=2, seed=41)
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)  # the step's own optimizer call; lr 0 keeps the weights
+    es.step(idx.to(dev), tg.to(dev), opt, step)
+    losses = es.last['losses'].cpu()
+    grads = {n: p.grad.detach().cpu() for n, p in model.named_parameters()}
+
+    d, s, q = oe.member_layout(pairs, 2, chunk=4)
+    offs = oe.step_offsets(ocfg, seed, step, pairs)
+    ref = torch.empty(len(d))
+    for seq in range(2):
+        sel = np.nonzero(q == seq)[0]
+        noise = oe.noise(ocfg, seed, offs, d[sel])
+        ref[sel] = om.population_loss(w, ocfg, noise, torch.tensor(s[sel] * sigma, dtype=torch.float32),
+                                      idx[seq], tg[seq]) / 256
+    assert ((losses - ref).abs() / ref).max().item() < 1e-2
+    weight = es.last['weight'].cpu()
+    assert torch.allclose(es.last['fitness'].cpu(), oe.fitness(losses), rtol=1e-4, atol=1e-4)
+    want = oe.gradients(ocfg, seed, offs, weight, n_fitness=len(d) // 2)
+    for name, gv in want.items():
+        err = (grads[name] - gv).abs().max().item() / max(gv.abs().max().item(), 1e-12)
+        assert err < 1e-4, (name, err)

@@ -1,0 +1,161 @@
+"""Pins of the fp32 model oracle (oracle/model.py): the golden fixtures written from the reference's own GPT.forward
+and population_loss (tests/golden/make_golden.py), the init-time closed form, textbook causal SDPA, and brute-force
+materialized perturbations. Each pin is checked to fail on a planted mistake in the oracle."""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model as om
+from tests.golden import recipe
+
+GOLDEN = Path(__file__).resolve().parent / 'golden'
+
+
+def _small():
+    cfg = om.Config(**recipe.SMALL)
+    return cfg, recipe.weights(cfg)
+
+
+def test_param_order_matches_reference():
+    order = json.loads((GOLDEN / 'param_order.json').read_text())
+    assert order == [[n, list(s)] for n, s in om.param_specs(om.Config())]
+    assert sum(math.prod(s) for _, s in om.param_specs(om.Config())) == 37_749_776
+    assert sum(sum(s) for _, s in om.param_specs(om.Config())) == 101_552
+
+
+def test_gpt_forward_golden():
+    cfg, w = _small()
+    idx, tg = recipe.tokens(cfg, batch=2, ignore_every=29)
+    g = np.load(GOLDEN / 'gpt_forward_small.npz')
+    ce = om.gpt_forward(w, cfg, idx, tg, 'none').numpy()
+    assert np.abs(ce - g['ce']).max() < 1e-5
+    logits = om.gpt_forward(w, cfg, idx)[0, [0, 31, 63]].numpy()
+    assert np.abs(logits - g['logits_b0']).max() < 1e-5
+
+
+def test_population_loss_golden():
+    cfg, w = _small()
+    g = np.load(GOLDEN / 'population_loss_small.npz')
+    sigma = float(g['sigma'])
+    noise = recipe.population_noise(cfg, 4)
+    sign = torch.tensor([sigma, -sigma, sigma, -sigma])
+    idx, tg = recipe.tokens(cfg, batch=1, seed=recipe.TOKEN_SEED + 1)
+    got = (om.population_loss(w, cfg, noise, sign, idx[0], tg[0]) / cfg.sequence_len).numpy()
+    assert np.abs(got - g['mean_ce']).max() < 1e-5
+
+
+def test_planted_rotary_sign_fails_golden(monkeypatch):
+    """A flipped rotary sign in the oracle must break the fixture comparison."""
+    cfg, w = _small()
+    idx, tg = recipe.tokens(cfg, batch=2, ignore_every=29)
+    g = np.load(GOLDEN / 'gpt_forward_small.npz')
+    real = om.apply_rotary
+    monkeypatch.setattr(om, 'apply_rotary', lambda x, c, s: real(x, c, -s))
+    ce = om.gpt_forward(w, cfg, idx, tg, 'none').numpy()
+    assert np.abs(ce - g['ce']).max() > 1e-3
+
+
+def test_planted_window_off_by_one_fails_golden(monkeypatch):
+    cfg, w = _small()
+    idx, tg = recipe.tokens(cfg, batch=2, ignore_every=29)
+    g = np.load(GOLDEN / 'gpt_forward_small.npz')
+    real = om.attention
+    monkeypatch.setattr(om, 'attention', lambda q, k, v, window: real(q, k, v, window - 1))
+    ce = om.gpt_forward(w, cfg, idx, tg, 'none').numpy()
+    assert np.abs(ce - g['ce']).max() > 1e-4
+
+
+def _init_weights(cfg, seed=0):
+    """utils/model.py:149-175's distributions: c_proj and ve_gate zero, lambdas 1 / 0.1."""
+    g = torch.Generator().manual_seed(seed)
+    s = 3 ** 0.5 * cfg.n_embd ** -0.5
+    w = {}
+    for name, shape in om.param_specs(cfg):
+        if name == 'resid_lambdas':
+            w[name] = torch.ones(shape)
+        elif name == 'x0_lambdas':
+            w[name] = torch.full(shape, 0.1)
+        elif 'wte' in name:
+            w[name] = torch.randn(shape, generator=g)
+        elif 'lm_head' in name:
+            w[name] = torch.randn(shape, generator=g) * 0.001
+        elif 'c_proj' in name or 've_gate' in name:
+            w[name] = torch.zeros(shape)
+        else:
+            w[name] = (torch.rand(shape, generator=g) * 2 - 1) * s
+    return w
+
+
+def test_init_closed_form():
+    """At init every block is the identity on the stream: x_L = (prod of the mixes) x0 = 1.8 x0 after 8 blocks (the
+    lambda mix x <- 1 x + 0.1 x0 applied 8 times); the final norm removes the scale, so the logits are
+    lm_head(norm(wte[idx])) and the CE has that closed form."""
+    cfg = om.Config(sequence_len=128)
+    w = _init_weights(cfg)
+    idx, tg = recipe.tokens(cfg, batch=1)
+    got = om.gpt_forward(w, cfg, idx, tg, 'none')
+    z = om.rms_norm(w['transformer.wte.weight'][idx]) @ w['lm_head.weight'].t()
+    z = 15 * torch.tanh(z / 15)
+    want = torch.logsumexp(z, -1) - z.gather(-1, tg.unsqueeze(-1)).squeeze(-1)
+    assert torch.allclose(got, want.reshape(-1), atol=1e-5)
+    # lm_head std 0.001: the loss is ln 4096 to within the tiny logits (the reference logs 8.319 at step 1)
+    assert abs(got.mean().item() - math.log(4096)) < 0.01
+
+
+def test_attention_full_window_is_causal_sdpa():
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(2, 96, 3, 64, generator=g) for _ in range(3))
+    got = om.attention(q, k, v, window=96)
+    want = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                          is_causal=True).transpose(1, 2)
+    assert torch.allclose(got, want, atol=1e-5)
+
+
+def test_attention_window_bruteforce():
+    g = torch.Generator().manual_seed(2)
+    T, W = 20, 5
+    q, k, v = (torch.randn(1, T, 1, 64, generator=g, dtype=torch.float64) for _ in range(3))
+    got = om.attention(q, k, v, W)[0, :, 0]
+    for s in range(T):
+        lo = max(0, s - W)
+        logits = torch.tensor([(q[0, s, 0] @ k[0, t, 0]).item() / 8 for t in range(lo, s + 1)], dtype=torch.float64)
+        p = torch.softmax(logits, 0)
+        want = sum(p[j] * v[0, lo + j, 0] for j in range(len(p)))
+        assert torch.allclose(got[s], want, atol=1e-10)
+
+
+def test_lowrank_bruteforce():
+    g = torch.Generator().manual_seed(3)
+    m, T, n_in, n_out = 3, 5, 7, 4
+    x = torch.randn(m, T, n_in, generator=g, dtype=torch.float64)
+    W = torch.randn(n_out, n_in, generator=g, dtype=torch.float64)
+    a, b = torch.randn(m, n_out, generator=g, dtype=torch.float64), torch.randn(m, n_in, generator=g, dtype=torch.float64)
+    sign = torch.tensor([0.1, -0.1, 0.3], dtype=torch.float64)
+    got = om.lowrank(x, W, a, b, sign)
+    for i in range(m):
+        assert torch.allclose(got[i], x[i] @ (W + sign[i] * torch.outer(a[i], b[i])).t())
+    V, d = 11, 6
+    E = torch.randn(V, d, generator=g, dtype=torch.float64)
+    ae, be = torch.randn(m, V, generator=g, dtype=torch.float64), torch.randn(m, d, generator=g, dtype=torch.float64)
+    idx = torch.tensor([3, 0, 10, 3])
+    emb = om.lowrank_embed(E, ae, be, idx, sign)
+    for i in range(m):
+        assert torch.allclose(emb[i], (E + sign[i] * torch.outer(ae[i], be[i]))[idx])
+
+
+def test_population_zero_sigma_is_gpt_forward():
+    cfg, w = _small()
+    idx, tg = recipe.tokens(cfg, batch=1)
+    noise = recipe.population_noise(cfg, 2)
+    pl = om.population_loss(w, cfg, noise, torch.zeros(2), idx[0], tg[0])
+    ref = om.gpt_forward(w, cfg, idx, tg, 'sum')
+    assert torch.allclose(pl, ref.expand(2), rtol=1e-5)
+
+
+def test_flops_per_member_token():
+    assert abs(om.flops_per_member_token(om.Config()) - 68.170752e6) < 1.0
