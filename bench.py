@@ -1,0 +1,280 @@
+#!/usr/bin/env python3
+"""Benchmark of the population hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload c4|c5] [--no-cpu-baseline] [--no-credit]
+
+A step is one pass of the hot path over one batch of synthetic input:
+  c4 (default): the 8-layer population forward of BASELINE config 4: 256 antithetic members (128 pairs), each
+      evaluating 2 sequences x 2048 Zipf(1.1) tokens over vocab 4096, weights N(0, 0.02) (lambdas 1 / 0.1), with the
+      per-step noise offsets and rows generated on the GPU; output per-member summed CE. 1,048,576 member-tokens.
+  c5: one full EGGROLL training step (config 5): 12,288 pairs = 24,576 members over an 8 x 2048 batch, chunks of
+      512 members, fitness, outer-product gradient assembly and AdamW. 50,331,648 member-tokens.
+The JSON line carries the metric of BASELINE.json, the roofline of the dominant kernel (HIP events on the launch
+stream over the timed region), the oracle's CPU throughput on a bounded sample, and the credit readout's TFLOP/s at
+config 3 (B16 H8 T2048 d64).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+METRIC = 'perturbed-forward tokens/sec (members×tokens) at 37.7M; credit kernel TFLOP/s'
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+FLOP_PER_MEMBER_TOKEN = 68.170752e6
+D, F, QKV, V, T_SEQ = 512, 2048, 1536, 4096, 2048
+
+
+def zipf_tokens(n_rows, T, seed, vocab=V, s=1.1):
+    import torch
+    p = (torch.arange(vocab, dtype=torch.float64) + 1.0) ** -s
+    cdf = torch.cumsum(p / p.sum(), 0)
+    u = torch.rand(n_rows, T + 1, generator=torch.Generator().manual_seed(seed), dtype=torch.float64)
+    rows = torch.searchsorted(cdf, u).clamp(max=vocab - 1)
+    return rows[:, :-1].contiguous(), rows[:, 1:].contiguous()
+
+
+def make_model(dev, seed=0):
+    import torch
+    from noise_amd.model import GPT, GPTConfig
+    torch.manual_seed(seed)
+    with torch.device('meta'):
+        model = GPT(GPTConfig())
+    model.to_empty(device=dev)
+    model.init_weights()
+    model.transformer.wte.float()
+    for e in model.value_embeds.values():
+        e.float()
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if p.dim() == 2:
+                p.normal_(0.0, 0.02)
+    return model.requires_grad_(False)
+
+
+def attention_flops(members_rows, windows, T):
+    tot = 0.0
+    for w in windows:
+        keys = sum(min(t, w) + 1 for t in range(T))
+        tot += 4 * D * keys
+    return tot * members_rows  # members_rows = evaluations (rows of T tokens)
+
+
+def kernel_flops(n_eval, T, windows, n_layer):
+    """Algorithmic FLOPs per launch of each timed kernel class (rank-1 terms excluded, in-window pairs only)."""
+    M = n_eval * T
+    return {
+        'qkv_gemm': 2.0 * M * QKV * D,
+        'attn_proj_gemm': 2.0 * M * D * D,
+        'fc_gemm': 2.0 * M * F * D,
+        'mlp_proj_gemm': 2.0 * M * D * F,
+        'head_ce_gemm': 2.0 * M * V * D,
+        'attention': attention_flops(n_eval, windows, T) / n_layer,
+    }
+
+
+def roofline_from_timing(timing, flops):
+    kernels = {}
+    for name, f in flops.items():
+        n, ms = timing.get(name, (0, 0.0))
+        if n == 0:
+            continue
+        avg_ms = ms / n
+        tf = f / (avg_ms * 1e-3) / 1e12
+        kernels[name] = dict(launches=n, avg_ms=round(avg_ms, 4), total_ms=round(ms, 3), tflops=round(tf, 1),
+                             frac=round(tf / PEAK_BF16_TFLOPS, 4))
+    dom = max(kernels, key=lambda k: kernels[k]['total_ms'])
+    k = kernels[dom]
+    roof = dict(bound='mfma', kernel=dom, achieved=k['tflops'], peak=PEAK_BF16_TFLOPS, unit='TFLOP/s', frac=k['frac'],
+                traffic=None, flop_per_launch=flops[dom], avg_launch_ms=k['avg_ms'])
+    return roof, kernels
+
+
+def bench_c4(args, dev):
+    import torch
+    from noise_amd import _lib
+    from noise_amd.population import Eggroll, NoiseLayout, run_forward
+    model = make_model(dev)
+    pairs, n_seq = 128, 2
+    members = 2 * pairs
+    x, y = zipf_tokens(n_seq, T_SEQ, seed=0)
+    x, y = x.to(dev), y.to(dev)
+    es = Eggroll(model, pairs, sigma=0.002, seed=0)
+    layout = NoiseLayout(model)
+    # evaluation e = (member e // 2, sequence e % 2): the member's pair direction and antithetic sign
+    ev = torch.arange(members * n_seq, device=dev)
+    member = ev // n_seq
+    member_seq = (ev % n_seq).to(torch.int32)
+    member_row = (member // 2).to(torch.int32)
+    member_sign = torch.where(member % 2 == 0, 0.002, -0.002).float()
+    all_dirs = torch.arange(pairs, device=dev)
+
+    def step(i):
+        table = es.offset_table(i)
+        rows = es.rows(table, all_dirs)
+        out = run_forward(model, x, y, member_seq, noise=rows, member_row=member_row, member_sign=member_sign,
+                          layout=layout)
+        return out['loss_sum'].view(members, n_seq).sum(1)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        losses = step(args.warmup + i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    timing = _lib.timing_read()
+    _lib.timing_enable(False)
+    finite = bool(torch.isfinite(losses).all().item())
+    member_tokens = members * n_seq * T_SEQ
+    windows = [w for w, _ in model.window_sizes]
+    roof, kernels = roofline_from_timing(timing, kernel_flops(members * n_seq, T_SEQ, windows, len(windows)))
+    res = dict(value=member_tokens * args.steps / dt, ms_per_step=dt / args.steps * 1e3, member_tokens=member_tokens,
+               roofline=roof, kernels=kernels, finite=finite,
+               mean_member_ce=float(losses.mean().item() / (n_seq * T_SEQ)),
+               config=dict(workload='C4: 8-layer population forward, 256 antithetic members (128 pairs) x 2 '
+                           'sequences x 2048 Zipf(1.1) tokens, vocab 4096, N(0,0.02) weights, in-kernel counter noise',
+                           members=members, sequences_per_member=n_seq, seq_len=T_SEQ, n_layer=len(windows),
+                           params=sum(p.numel() for p in model.parameters()), parallelism='single GPU'))
+    res['model'] = model
+    return res
+
+
+def bench_c5(args, dev):
+    import torch
+    from noise_amd import _lib
+    from noise_amd.optim import AdamW
+    from noise_amd.population import Eggroll
+    model = make_model(dev)
+    pairs, n_seq = 12288, 8
+    x, y = zipf_tokens(n_seq, T_SEQ, seed=0)
+    x, y = x.to(dev), y.to(dev)
+    es = Eggroll(model, pairs, sigma=0.002, seed=0, chunk=256)
+    opt = AdamW(model.parameters(), lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    for i in range(args.warmup):
+        es.step(x, y, opt, i + 1)
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        loss = es.step(x, y, opt, args.warmup + i + 1)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    timing = _lib.timing_read()
+    _lib.timing_enable(False)
+    members = 2 * pairs
+    member_tokens = members * T_SEQ
+    windows = [w for w, _ in model.window_sizes]
+    roof, kernels = roofline_from_timing(timing, kernel_flops(2 * es.chunk, T_SEQ, windows, len(windows)))
+    res = dict(value=member_tokens * args.steps / dt, ms_per_step=dt / args.steps * 1e3, member_tokens=member_tokens,
+               roofline=roof, kernels=kernels, finite=math.isfinite(loss), mean_member_ce=loss,
+               config=dict(workload='C5: full EGGROLL step, 24,576 members (12,288 pairs) in chunks of 512 over an '
+                           '8 x 2048 Zipf(1.1) batch, fitness, outer-product gradients, AdamW',
+                           members=members, seq_len=T_SEQ, n_layer=len(windows), parallelism='single GPU'))
+    res['model'] = model
+    return res
+
+
+def bench_credit(dev, iters=10):
+    """Config 3: lse + value pass, B16 H8 T2048 d64, Q/K bf16 N(0,1)/8, E N(0,1) fp32, full causal window."""
+    import torch
+    from noise_amd import _lib, credit
+    rows, T = 16 * 8, 2048
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = (torch.randn(rows, T, 64, device=dev, generator=g) / 8).bfloat16()
+    k = (torch.randn(rows, T, 64, device=dev, generator=g) / 8).bfloat16()
+    e = torch.randn(rows, T, 64, device=dev, generator=g)
+    pairs = rows * T * (T + 1) // 2
+    out = {}
+    for window in (T, 1024):
+        npairs = rows * sum(min(t, window) + 1 for t in range(T))
+        for _ in range(2):
+            credit.value_credit(q, k, e, window)
+        torch.cuda.synchronize()
+        _lib.timing_enable(True)
+        for _ in range(iters):
+            credit.value_credit(q, k, e, window)
+        torch.cuda.synchronize()
+        tm = _lib.timing_read()
+        _lib.timing_enable(False)
+        lse_ms = tm['credit_lse'][1] / tm['credit_lse'][0]
+        val_ms = tm['credit_value'][1] / tm['credit_value'][0]
+        flops = 6 * 64 * npairs
+        out[f'window_{window}'] = dict(
+            pairs=npairs, tflops=round(flops / ((lse_ms + val_ms) * 1e-3) / 1e12, 1),
+            frac=round(flops / ((lse_ms + val_ms) * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            lse_ms=round(lse_ms, 4), value_ms=round(val_ms, 4),
+            value_pass_tflops=round(4 * 64 * npairs / (val_ms * 1e-3) / 1e12, 1))
+    out['headline'] = f"{out[f'window_{T}']['tflops']} TFLOP/s at 6d per causal pair ({pairs:,} pairs)"
+    return out
+
+
+def cpu_baseline(model, sample_members=4, T=T_SEQ, reps=3):
+    """The oracle (fp32 eager torch on the host cores) on a bounded sample of the same population forward."""
+    import torch
+    from oracle import eggroll as oe
+    from oracle import model as om
+    ocfg = om.Config()
+    w = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    pairs = sample_members // 2
+    offs = oe.step_offsets(ocfg, 0, 0, pairs)
+    noise = oe.noise(ocfg, 0, offs, [j // 2 for j in range(sample_members)])
+    sign = torch.tensor([0.002 if j % 2 == 0 else -0.002 for j in range(sample_members)])
+    x, y = zipf_tokens(1, T, seed=0)
+    times = []
+    with torch.no_grad():
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            om.population_loss(w, ocfg, noise, sign, x[0], y[0])
+            if r:
+                times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return dict(value=round(sample_members * T / med, 1), unit='member-tokens/s', cores=torch.get_num_threads(),
+                kind='port', sample=f'{sample_members} members ({pairs} antithetic pairs) x 1 sequence x {T} tokens '
+                f'of the same population forward, oracle/model.py fp32 eager torch; median of {reps} after 1 warmup '
+                f'({med:.2f} s each)')
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=10)
+    ap.add_argument('--warmup', type=int, default=2)
+    ap.add_argument('--workload', choices=['c4', 'c5'], default='c4')
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-credit', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
+        sys.exit('bench.py measures one GPU: this build runs the hot path on a single MI355X; '
+                 'multi-GPU member sharding is design-only (see --gpus 1)')
+    import torch
+    from noise_amd import _lib
+    _lib.lib()
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    res = bench_c4(args, dev) if args.workload == 'c4' else bench_c5(args, dev)
+    model = res.pop('model')
+    line = dict(metric=METRIC, value=round(res['value'], 1), unit='member-tokens/s', n_gpus=1, steps=args.steps,
+                warmup=args.warmup, ms_per_step=round(res['ms_per_step'], 3), higher_is_better=True, scaling='weak',
+                vs_baseline=None, dtype='bf16', data='synthetic (Zipf(1.1) tokens, random-init weights)',
+                config=res['config'], roofline=res['roofline'])
+    line['roofline']['forward_tflops'] = round(res['value'] * FLOP_PER_MEMBER_TOKEN / 1e12, 1)
+    line['roofline']['forward_frac'] = round(res['value'] * FLOP_PER_MEMBER_TOKEN / 1e12 / PEAK_BF16_TFLOPS, 4)
+    line['kernels'] = res['kernels']
+    line['finite'] = res['finite']
+    if not args.no_credit:
+        line['credit'] = bench_credit(dev)
+    if not args.no_cpu_baseline:
+        line['cpu_baseline'] = cpu_baseline(model)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

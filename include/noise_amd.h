@@ -27,6 +27,13 @@ const char* noise_last_error(void);
 /* ABI version (bumped on any signature change). */
 int noise_abi_version(void);
 
+/* Launch timing for measurement (no counterpart in the reference, whose kernels are timed with CUDA events from
+ * Python: train/speedrun/run.py:4262, 4316): noise_timing_enable(1) clears the figures and brackets every following
+ * launch with hipEvents on its stream; noise_timing_read() waits for them and returns per-class launch counts and
+ * summed milliseconds (arrays of n entries) and the class names; it returns the number of classes. */
+int noise_timing_enable(int enable);
+int noise_timing_read(int32_t n, int64_t* counts, double* total_ms, const char** names);
+
 /* ---- a1: counter-based noise (replaces the 2^28-value torch.randn buffer and the torch.randint offsets) -------- */
 
 /* out[j] = G[start + j], the virtual N(0,1) buffer of Philox4x32-10 + Box-Muller values.

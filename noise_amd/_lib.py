@@ -37,6 +37,8 @@ class NoisePerturbation(ctypes.Structure):
 _SIGNATURES = {
     'noise_last_error': ([], ctypes.c_char_p),
     'noise_abi_version': ([], ctypes.c_int),
+    'noise_timing_enable': ([ctypes.c_int], ctypes.c_int),
+    'noise_timing_read': ([i32, c_p, c_p, c_p], ctypes.c_int),
     'noise_rng_buffer': ([u64, u64, i64, c_p, c_p], ctypes.c_int),
     'noise_rng_offsets': ([u64, u64, c_p, i32, i64, c_p, c_p], ctypes.c_int),
     'noise_rng_rows': ([u64, c_p, i64, c_p, i32, c_p, i64, c_p, c_p], ctypes.c_int),
@@ -101,3 +103,17 @@ def require_device(*tensors):
     for t in tensors:
         if t is not None and t.device.type != 'cuda':
             raise ValueError(f'noise_amd kernels take device tensors, got a tensor on {t.device}')
+
+
+def timing_enable(on=True):
+    lib().noise_timing_enable(int(on))
+
+
+def timing_read():
+    """class name -> (launch count, total milliseconds) of the launches timed since timing_enable()."""
+    n = 32
+    counts = (ctypes.c_int64 * n)()
+    ms = (ctypes.c_double * n)()
+    names = (ctypes.c_char_p * n)()
+    k = lib().noise_timing_read(n, counts, ms, names)
+    return {names[c].decode(): (counts[c], ms[c]) for c in range(k)}

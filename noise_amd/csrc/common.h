@@ -66,3 +66,18 @@ int noise_set_error(int code, const char* fmt, ...);
   } while (0)
 
 #define NOISE_LAUNCH_CHECK() NOISE_CHECK_HIP(hipGetLastError())
+
+// Per-kernel-class launch timing (diagnostics, off by default): when enabled, launches are bracketed by hipEvent
+// pairs recorded on their stream; noise_timing_read() reports counts and summed durations per class.
+enum NoiseTimingClass {
+  kTimeNoise = 0, kTimeEmbed, kTimeNorm, kTimeQKV, kTimeRope, kTimeAttention, kTimeProj, kTimeFc, kTimeRowdot,
+  kTimeMlpProj, kTimeHead, kTimeCeFinal, kTimeCreditLse, kTimeCreditValue, kTimeUpdate, kTimeLowrank,
+  kTimeClasses
+};
+
+struct NoiseTimer {
+  int slot;
+  hipStream_t stream;
+  NoiseTimer(int cls, hipStream_t s);
+  ~NoiseTimer();
+};

@@ -542,8 +542,11 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
   const bool noisy = pert->rows != nullptr;
   const unsigned row_blocks = (unsigned)((M + 3) / 4);
 
-  hipLaunchKernelGGL(embed_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte, ws.x0, M);
-  NOISE_LAUNCH_CHECK();
+  {
+    NoiseTimer tm(kTimeEmbed, stream);
+    hipLaunchKernelGGL(embed_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte, ws.x0, M);
+    NOISE_LAUNCH_CHECK();
+  }
 
   for (int i = 0; i < model->n_layer; ++i) {
     const noise_layer& L = model->layers[i];
@@ -559,15 +562,24 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     na.h = ws.h; na.ndot = 3;
     na.off_b[0] = pert->c_q[i] + kD; na.off_b[1] = pert->c_k[i] + kD; na.off_b[2] = pert->c_v[i] + kD;
     na.xb = ws.xb; na.w_gate = L.w_gate; na.off_gate = pert->ve_gate[i]; na.gate = ws.gate; na.M = M;
-    hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, na);
-    NOISE_LAUNCH_CHECK();
+    {
+      NoiseTimer tm(kTimeNorm, stream);
+      hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, na);
+      NOISE_LAUNCH_CHECK();
+    }
 
     EpiQKV eq{mb, ws.qkv, {pert->c_q[i], pert->c_k[i], pert->c_v[i]}, ws.xb, L.w_gate ? ws.gate : nullptr, L.ve,
               pert->ve[i], Vp};
-    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_qkv, kD, (int)M, kQKV, kD, eq, stream)));
-    hipLaunchKernelGGL(rope_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, ws.qkv, model->rope_cos,
-                       model->rope_sin, (int)T, M);
-    NOISE_LAUNCH_CHECK();
+    {
+      NoiseTimer tm(kTimeQKV, stream);
+      NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_qkv, kD, (int)M, kQKV, kD, eq, stream)));
+    }
+    {
+      NoiseTimer tm(kTimeRope, stream);
+      hipLaunchKernelGGL(rope_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, ws.qkv, model->rope_cos,
+                         model->rope_sin, (int)T, M);
+      NOISE_LAUNCH_CHECK();
+    }
 
     FlashArgs fa;
     memset(&fa, 0, sizeof(fa));
@@ -578,42 +590,65 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     fa.xb_vec = noisy ? pert->rows + pert->c_proj[i] + kD : nullptr;
     fa.xb_row = member_row; fa.xb_stride = pert->stride;
     fa.heads = kH; fa.T = (int)T; fa.window = L.window;
-    hipLaunchKernelGGL(window_flash_kernel<kAttn>, dim3((unsigned)(T / kFlashBO), kH, (unsigned)members), dim3(256), 0,
-                       stream, fa);
-    NOISE_LAUNCH_CHECK();
+    {
+      NoiseTimer tm(kTimeAttention, stream);
+      hipLaunchKernelGGL(window_flash_kernel<kAttn>, dim3((unsigned)(T / kFlashBO), kH, (unsigned)members), dim3(256),
+                         0, stream, fa);
+      NOISE_LAUNCH_CHECK();
+    }
 
     EpiResid ep{mb, ws.x, kD, pert->c_proj[i], ws.xbp, kH};
-    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
+    {
+      NoiseTimer tm(kTimeProj, stream);
+      NOISE_CHECK_HIP((launch_gemm<Tile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
+    }
 
     NormArgs nb;
     memset(&nb, 0, sizeof(nb));
     nb.x = ws.x; nb.h = ws.h; nb.ndot = 1; nb.off_b[0] = pert->c_fc[i] + kF;  // c_fc's a spans its 2048 outputs
     nb.xb = ws.xb; nb.M = M;
-    hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nb);
-    NOISE_LAUNCH_CHECK();
+    {
+      NoiseTimer tm(kTimeNorm, stream);
+      hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nb);
+      NOISE_LAUNCH_CHECK();
+    }
 
     EpiReluSq er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4};
-    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
+    {
+      NoiseTimer tm(kTimeFc, stream);
+      NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
+    }
     if (noisy) {
+      NoiseTimer tm(kTimeRowdot, stream);
       hipLaunchKernelGGL(rowdot_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, ws.hid, (int64_t)kF, kF,
                          pert->mlp_proj[i] + kD, ws.xb1, M);
       NOISE_LAUNCH_CHECK();
     }
     EpiResid em{mb, ws.x, kD, pert->mlp_proj[i], ws.xb1, 1};
-    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+    {
+      NoiseTimer tm(kTimeMlpProj, stream);
+      NOISE_CHECK_HIP((launch_gemm<Tile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+    }
   }
 
   NormArgs nf;
   memset(&nf, 0, sizeof(nf));
   nf.x = ws.x; nf.h = ws.h; nf.ndot = 1; nf.off_b[0] = pert->lm_head + Vp; nf.xb = ws.xb; nf.M = M;
-  hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nf);
-  NOISE_LAUNCH_CHECK();
+  {
+    NoiseTimer tm(kTimeNorm, stream);
+    hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nf);
+    NOISE_LAUNCH_CHECK();
+  }
 
   const int n_part = Vp / Tile::BN;
   const int64_t* tg = targets ? targets : tokens;  // logits-only calls still run the CE bookkeeping on tokens
   EpiHeadCE eh{mb, pert->lm_head, ws.xb, 4, model->vocab, n_part, ws.pmax, ws.psum, ws.tgt, tg, logits};
-  NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, model->lm_head, kD, (int)M, Vp, kD, eh, stream)));
+  {
+    NoiseTimer tm(kTimeHead, stream);
+    NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, model->lm_head, kD, (int)M, Vp, kD, eh, stream)));
+  }
   if (targets && (loss_sum || token_loss)) {
+    NoiseTimer tm(kTimeCeFinal, stream);
     hipLaunchKernelGGL(ce_finalize_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, stream, mb, ws.pmax,
                        ws.psum, n_part, ws.tgt, targets, model->vocab, ws.row_ce, token_loss, M);
     NOISE_LAUNCH_CHECK();

@@ -98,6 +98,7 @@ extern "C" int noise_attention(const uint16_t* q, const uint16_t* k, const uint1
   a.out = out; a.o_sb = out_stride_b; a.o_st = out_stride_t;
   a.lse_out = lse;
   a.heads = heads; a.T = (int)T; a.window = window;
+  NoiseTimer tm(kTimeAttention, (hipStream_t)stream);
   hipLaunchKernelGGL(window_flash_kernel<kAttn>, dim3((unsigned)(T / kFlashBO), (unsigned)heads, (unsigned)batch),
                      dim3(256), 0, (hipStream_t)stream, a);
   NOISE_LAUNCH_CHECK();
@@ -116,6 +117,7 @@ extern "C" int noise_credit_lse(const uint16_t* q, const uint16_t* k, int64_t ro
   a.x_sb = a.y_sb = T * 64; a.x_st = a.y_st = 64;
   a.lse_out = lse;
   a.heads = 1; a.T = (int)T; a.window = window;
+  NoiseTimer tm(kTimeCreditLse, (hipStream_t)stream);
   hipLaunchKernelGGL(window_flash_kernel<kLse>, dim3((unsigned)(T / kFlashBO), 1, (unsigned)rows), dim3(256), 0,
                      (hipStream_t)stream, a);
   NOISE_LAUNCH_CHECK();
@@ -135,6 +137,7 @@ extern "C" int noise_credit_value(const uint16_t* q, const uint16_t* k, const fl
   a.lse_in = lse;
   a.out = out; a.o_sb = T * 64; a.o_st = 64;
   a.heads = 1; a.T = (int)T; a.window = window; a.hi_lo = hi_lo;
+  NoiseTimer tm(kTimeCreditValue, (hipStream_t)stream);
   hipLaunchKernelGGL(window_flash_kernel<kCredit>, dim3((unsigned)(T / kFlashBO), 1, (unsigned)rows), dim3(256), 0,
                      (hipStream_t)stream, a);
   NOISE_LAUNCH_CHECK();
@@ -177,7 +180,10 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
   NOISE_LAUNCH_CHECK();
   EpiLowrank epi{(int)T, noise, noise_stride, a_off, sign, u, y, out, sumsq ? part : nullptr};
   NOISE_CHECK_HIP((prepare_gemm<LTile, EpiLowrank>()));
-  NOISE_CHECK_HIP((launch_gemm<LTile>(A, in, w, in, (int)M, (int)out, (int)in, epi, stream)));
+  {
+    NoiseTimer tm(kTimeLowrank, stream);
+    NOISE_CHECK_HIP((launch_gemm<LTile>(A, in, w, in, (int)M, (int)out, (int)in, epi, stream)));
+  }
   if (sumsq) {
     hipLaunchKernelGGL(member_part_sum_kernel, dim3((unsigned)m), dim3(64), 0, stream, part, (int)(T / LTile::BM),
                        (int)(out / LTile::BN), sumsq);

@@ -130,6 +130,7 @@ extern "C" int noise_rng_rows(uint64_t seed, const int64_t* offsets, int64_t pai
   const int64_t stride = a.col0[n_params - 1] + a.width[n_params - 1];
   const unsigned bx = (unsigned)((a.slot0[n_params] + 255) / 256);
   const unsigned by = (unsigned)(n < 65535 ? n : 65535);
+  NoiseTimer tm(kTimeNoise, (hipStream_t)stream);
   hipLaunchKernelGGL(rows_kernel, dim3(bx, by), dim3(256), 0, (hipStream_t)stream, seed, offsets, pairs, a, directions,
                      n, stride, rows);
   NOISE_LAUNCH_CHECK();

@@ -153,6 +153,7 @@ extern "C" int noise_outer_grad(const float* rows, int64_t stride, int64_t a_off
                                 int64_t pairs, int64_t out, int64_t in, float scale, float* grad, void* stream) {
   NOISE_REQUIRE(rows && weight && grad, "NULL pointer argument");
   NOISE_REQUIRE(pairs > 0 && in > 0 && a_off >= 0 && stride > 0, "bad sizes");
+  NoiseTimer tm(kTimeUpdate, (hipStream_t)stream);
   if (b_off < 0) {
     NOISE_REQUIRE(a_off + in <= stride, "slice beyond the noise row");
     hipLaunchKernelGGL(vector_grad_kernel, dim3((unsigned)((in + 255) / 256)), dim3(256), 0, (hipStream_t)stream, rows,

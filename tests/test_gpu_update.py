@@ -20,7 +20,8 @@ def test_fitness(dev):
         L = torch.from_numpy(r.normal(8.3, 0.05, members).astype(np.float32))
         f = torch.empty(members // 2, device=dev)
         w = torch.empty(pairs, device=dev)
-        _lib.call('noise_fitness', _lib.ptr(L.to(dev)), members, pairs, _lib.ptr(f), _lib.ptr(w), _lib.stream(dev))
+        L_d = L.to(dev)
+        _lib.call('noise_fitness', _lib.ptr(L_d), members, pairs, _lib.ptr(f), _lib.ptr(w), _lib.stream(dev))
         fr = oe.fitness(L)
         wr = oe.direction_weights(fr, pairs)
         assert torch.allclose(f.cpu(), fr, rtol=1e-4, atol=1e-4)
@@ -34,12 +35,13 @@ def test_outer_grad_and_vector_grad(dev):
     rows = torch.randn(pairs, stride, generator=g)
     w = torch.randn(pairs, generator=g)
     grad = torch.empty(out, n_in, device=dev)
-    _lib.call('noise_outer_grad', _lib.ptr(rows.to(dev)), stride, 5, 5 + out, _lib.ptr(w.to(dev)), pairs, out, n_in,
+    rows_d, w_d = rows.to(dev), w.to(dev)  # held: a freed temporary's block could be reused before the launch
+    _lib.call('noise_outer_grad', _lib.ptr(rows_d), stride, 5, 5 + out, _lib.ptr(w_d), pairs, out, n_in,
               -0.25, _lib.ptr(grad), _lib.stream(dev))
     want = -0.25 * (w[:, None] * rows[:, 5:5 + out]).t().double() @ rows[:, 5 + out:5 + out + n_in].double()
     assert torch.allclose(grad.cpu().double(), want, rtol=1e-4, atol=1e-4)
     vec = torch.empty(8, device=dev)
-    _lib.call('noise_outer_grad', _lib.ptr(rows.to(dev)), stride, 3, -1, _lib.ptr(w.to(dev)), pairs, 1, 8, 2.0,
+    _lib.call('noise_outer_grad', _lib.ptr(rows_d), stride, 3, -1, _lib.ptr(w_d), pairs, 1, 8, 2.0,
               _lib.ptr(vec), _lib.stream(dev))
     assert torch.allclose(vec.cpu(), 2.0 * (w @ rows[:, 3:11]), rtol=1e-4, atol=1e-4)
 
