@@ -24,18 +24,13 @@ constexpr int kQKV = 3 * kD;  // fused q|k|v output width
 
 __device__ __forceinline__ float bf16_to_f32(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet), the rounding of torch's .to(torch.bfloat16).
-__host__ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u;
-#if defined(__HIP_DEVICE_COMPILE__)
-  u = __float_as_uint(f);
-#else
-  union { float f; uint32_t u; } c; c.f = f; u = c.u;
-#endif
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (bf16_t)((u >> 16) | 0x40);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
-}
+// Round-to-nearest-even fp32 -> bf16, the rounding of torch's .to(torch.bfloat16) (gfx950 converts in hardware).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+// Hardware 2^x and 1/x (v_exp_f32, v_rcp_f32: about 1 ulp, no denormal-range fix-ups), for softmax weights and
+// soft caps whose arguments are bounded.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
 __device__ __forceinline__ float warp_sum(float v) {
 #pragma unroll

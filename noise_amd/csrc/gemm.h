@@ -71,11 +71,18 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
                                                               const bf16_t* __restrict__ B, int64_t ldb, int M, int N,
                                                               int K, Epi epi) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  // stage s: A tile at lds + s * kStage, B tile at lds + s * kStage + BM * BK (offsets, not a pointer array, so the
+  // accesses stay ds_read / ds_write)
   bf16_t* lds = (bf16_t*)smem_raw;
-  bf16_t* As[2] = {lds, lds + S::BM * S::BK};
-  bf16_t* Bs[2] = {lds + 2 * S::BM * S::BK, lds + 2 * S::BM * S::BK + S::BN * S::BK};
+  constexpr int kStage = (S::BM + S::BN) * S::BK;
 
-  const int m0 = blockIdx.y * S::BM, n0 = blockIdx.x * S::BN;
+  // Workgroups are dispatched round-robin over the 8 XCDs; tiles are renumbered so that each XCD walks a contiguous
+  // run of tiles in row-panel order (the A panel of a row tile is then fetched into one XCD's L2).
+  const int nt = gridDim.x, total = gridDim.x * gridDim.y;
+  const int bid = blockIdx.y * nt + blockIdx.x;
+  const int tile = (total % 8 == 0) ? (bid % 8) * (total / 8) + bid / 8 : bid;
+  const int m_tile = tile / nt, n_tile = tile % nt;
+  const int m0 = m_tile * S::BM, n0 = n_tile * S::BN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / S::WN, wn = wave % S::WN;
   const int a_rows = min(S::BM, M - m0), b_rows = min(S::BN, N - n0);
@@ -91,8 +98,8 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   u32x4 ra[S::kAVec], rb[S::kBVec];
   load_tile<S, S::kAVec>(A, lda, m0, a_rows, 0, ra);
   load_tile<S, S::kBVec>(B, ldb, n0, b_rows, 0, rb);
-  store_tile<S, S::kAVec>(As[0], ra);
-  store_tile<S, S::kBVec>(Bs[0], rb);
+  store_tile<S, S::kAVec>(lds, ra);
+  store_tile<S, S::kBVec>(lds + S::BM * S::BK, rb);
   __syncthreads();
 
   const int nk = K / S::BK;
@@ -102,28 +109,40 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
       load_tile<S, S::kAVec>(A, lda, m0, a_rows, (kt + 1) * S::BK, ra);
       load_tile<S, S::kBVec>(B, ldb, n0, b_rows, (kt + 1) * S::BK, rb);
     }
-    const bf16_t* as = As[cur];
-    const bf16_t* bs = Bs[cur];
+    const bf16_t* as = lds + cur * kStage;
+    const bf16_t* bs = as + S::BM * S::BK;
+    // fragments of k-substep kk + 1 are read while the MFMAs of kk run
+    bf16x8 fa[2][S::TM], fb[2][S::TN];
+#pragma unroll
+    for (int i = 0; i < S::TM; ++i) fa[0][i] = read_frag<S>(as, wm * S::WTM + i * 32 + (lane & 31), (lane >> 5));
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j) fb[0][j] = read_frag<S>(bs, wn * S::WTN + j * 32 + (lane & 31), (lane >> 5));
 #pragma unroll
     for (int kk = 0; kk < S::BK / 16; ++kk) {
-      bf16x8 fa[S::TM], fb[S::TN];
+      const int c = kk & 1;
+      if (kk + 1 < S::BK / 16) {
 #pragma unroll
-      for (int i = 0; i < S::TM; ++i) fa[i] = read_frag<S>(as, wm * S::WTM + i * 32 + (lane & 31), kk * 2 + (lane >> 5));
+        for (int i = 0; i < S::TM; ++i)
+          fa[c ^ 1][i] = read_frag<S>(as, wm * S::WTM + i * 32 + (lane & 31), (kk + 1) * 2 + (lane >> 5));
 #pragma unroll
-      for (int j = 0; j < S::TN; ++j) fb[j] = read_frag<S>(bs, wn * S::WTN + j * 32 + (lane & 31), kk * 2 + (lane >> 5));
+        for (int j = 0; j < S::TN; ++j)
+          fb[c ^ 1][j] = read_frag<S>(bs, wn * S::WTN + j * 32 + (lane & 31), (kk + 1) * 2 + (lane >> 5));
+      }
 #pragma unroll
       for (int i = 0; i < S::TM; ++i)
 #pragma unroll
         for (int j = 0; j < S::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][i], fb[c][j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < nk) {
-      store_tile<S, S::kAVec>(As[cur ^ 1], ra);
-      store_tile<S, S::kBVec>(Bs[cur ^ 1], rb);
+      store_tile<S, S::kAVec>(lds + (cur ^ 1) * kStage, ra);
+      store_tile<S, S::kBVec>(lds + (cur ^ 1) * kStage + S::BM * S::BK, rb);
     }
     __syncthreads();
   }
-  epi.template apply<S>(acc, m0 + wm * S::WTM, n0 + wn * S::WTN, lane, (void*)smem_raw);
+  // A wave tile (WTM rows) lies in one member when T % WTM == 0; past-the-end waves only join the epilogue's barriers.
+  const bool valid = m0 + wm * S::WTM < M;
+  epi.template apply<S>(acc, m0 + wm * S::WTM, n0 + wn * S::WTN, lane, (void*)smem_raw, m_tile, n_tile, valid);
 }
 
 // Row / column of accumulator element (i, j, r) for this lane.

@@ -16,9 +16,11 @@ struct EpiLowrank {
   const float* u;     // [M] x . b of each row
   float* y;           // [M, N] or NULL
   int64_t ldy;
-  float* part;        // [M / BM, N / BN] partial sums of y^2 or NULL
+  float* part;        // [M / WTM, N / WTN] per-wave-tile partial sums of y^2, or NULL
   template <class S>
-  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void* smem) const {
+  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*, int, int,
+                                        bool valid) const {
+    if (!valid) return;
     const int m = row0 / T;
     const float s = sign[m];
     const float* nr = noise + (int64_t)m * stride + a_off;
@@ -39,14 +41,7 @@ struct EpiLowrank {
     }
     if (!part) return;
     ss = warp_sum(ss);
-    float* red = (float*)smem;
-    if (lane == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float t = 0.f;
-      for (int w = 0; w < S::kThreads / 64; ++w) t += red[w];
-      part[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = t;
-    }
+    if (lane == 0) part[(int64_t)(row0 / S::WTM) * (gridDim.x * S::WN) + col0 / S::WTN] = ss;
   }
 };
 
@@ -65,7 +60,7 @@ __global__ __launch_bounds__(256) void lowrank_u_kernel(const bf16_t* __restrict
   if (lane == 0) u[r] = d;
 }
 
-// sumsq[m] = sum of the member's tile partials, fixed order.
+// sumsq[m] = sum of the member's wave-tile partials, fixed order.
 __global__ void member_part_sum_kernel(const float* __restrict__ part, int tiles_per_member, int tiles_x,
                                        float* __restrict__ out) {
   const int m = blockIdx.x;
@@ -76,7 +71,7 @@ __global__ void member_part_sum_kernel(const float* __restrict__ part, int tiles
   out[m] = s;
 }
 
-using LTile = GemmShape<128, 128, 64, 2, 2>;
+using LTile = GemmShape<256, 256, 64, 2, 2>;
 
 }  // namespace noise
 
@@ -149,7 +144,7 @@ static inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 extern "C" size_t noise_lowrank_workspace(int64_t m, int64_t T, int64_t in, int64_t out, int32_t x_shared) {
   (void)in; (void)x_shared;
   const int64_t M = m * T;
-  const int64_t tiles = (M / LTile::BM) * (out / LTile::BN);
+  const int64_t tiles = ((M + LTile::BM - 1) / LTile::BM * LTile::WM) * (out / LTile::WTN);
   return al256((size_t)M * 4) + al256((size_t)tiles * 4) + (x_shared ? al256((size_t)M * in * 2) : 0);
 }
 
@@ -159,9 +154,9 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
                              void* stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   NOISE_REQUIRE(x && w && noise && sign, "NULL pointer argument");
-  NOISE_REQUIRE(m > 0 && T > 0 && T % LTile::BM == 0, "T = %lld must be a positive multiple of %d", (long long)T,
-                LTile::BM);
-  NOISE_REQUIRE(in > 0 && in % LTile::BK == 0 && out > 0 && out % LTile::BN == 0, "in %% 64 and out %% 128 must be 0");
+  NOISE_REQUIRE(m > 0 && T > 0 && T % LTile::WTM == 0, "T = %lld must be a positive multiple of %d", (long long)T,
+                LTile::WTM);
+  NOISE_REQUIRE(in > 0 && in % LTile::BK == 0 && out > 0 && out % LTile::BN == 0, "in %% 64 and out %% 256 must be 0");
   const int64_t M = m * T;
   NOISE_REQUIRE(M <= (int64_t)INT32_MAX / 4, "m * T too large");
   NOISE_REQUIRE(workspace && workspace_bytes >= noise_lowrank_workspace(m, T, in, out, x_shared),
@@ -170,7 +165,8 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
   float* part = (float*)((char*)workspace + al256((size_t)M * 4));
   const bf16_t* A = (const bf16_t*)x;
   if (x_shared) {  // replicate the shared operand per member (workspace), so the grouped GEMM streams one [M, in] A
-    bf16_t* rep = (bf16_t*)((char*)part + al256((size_t)(M / LTile::BM) * (out / LTile::BN) * 4));
+    bf16_t* rep = (bf16_t*)((char*)part + al256((size_t)((M + LTile::BM - 1) / LTile::BM * LTile::WM) *
+                                                 (out / LTile::WTN) * 4));
     for (int64_t i = 0; i < m; ++i)
       NOISE_CHECK_HIP(hipMemcpyAsync(rep + i * T * in, x, (size_t)T * in * 2, hipMemcpyDeviceToDevice, stream));
     A = rep;
@@ -185,8 +181,8 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
     NOISE_CHECK_HIP((launch_gemm<LTile>(A, in, w, in, (int)M, (int)out, (int)in, epi, stream)));
   }
   if (sumsq) {
-    hipLaunchKernelGGL(member_part_sum_kernel, dim3((unsigned)m), dim3(64), 0, stream, part, (int)(T / LTile::BM),
-                       (int)(out / LTile::BN), sumsq);
+    hipLaunchKernelGGL(member_part_sum_kernel, dim3((unsigned)m), dim3(64), 0, stream, part, (int)(T / LTile::WTM),
+                       (int)(out / LTile::WTN), sumsq);
     NOISE_LAUNCH_CHECK();
   }
   return NOISE_OK;

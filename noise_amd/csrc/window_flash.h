@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) void window_flash_kernel(FlashArgs a) {
           const int i = i0 + il;
           const bool ok = full || ((i - my_o) >= 0 && (i - my_o) <= W && i < T);
           const float e = s[t][r] * qk_scale - lse_s[il] * kLog2e;
-          s[t][r] = ok ? exp2f(e) : 0.f;
+          s[t][r] = ok ? fast_exp2(e) : 0.f;
         }
     } else {
       float mt = -INFINITY;
@@ -189,13 +189,13 @@ __global__ __launch_bounds__(256) void window_flash_kernel(FlashArgs a) {
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
       const float m_new = fmaxf(m_run, mt);
       const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
-      const float corr = exp2f(m_run - m_safe);
+      const float corr = fast_exp2(m_run - m_safe);
       float ls = 0.f;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = exp2f(s[t][r] - m_safe);
+          const float p = fast_exp2(s[t][r] - m_safe);
           s[t][r] = p;
           ls += p;
         }

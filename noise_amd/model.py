@@ -168,8 +168,8 @@ class GPT(nn.Module):
             raise ValueError('the HIP kernels are built for the fixed model: n_embd 512, 8 heads of 64')
         if c.n_layer > _lib.MAX_LAYERS:
             raise ValueError(f'n_layer {c.n_layer} > {_lib.MAX_LAYERS}')
-        if self.lm_head.weight.shape[0] % 128 or self.lm_head.weight.shape[0] > 4096:
-            raise ValueError('padded vocabulary must be a multiple of 128 and at most 4096')
+        if self.lm_head.weight.shape[0] % 256 or self.lm_head.weight.shape[0] > 4096:
+            raise ValueError('padded vocabulary must be a multiple of 256 and at most 4096')
 
     def packed(self):
         """bf16 GEMM operands, fp32 tables and the ctypes model struct; rebuilt when any parameter changed."""
