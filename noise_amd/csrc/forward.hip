@@ -1,8 +1,7 @@
 // The perturbed population forward of the fixed GPT (archive/10M/train/val/eggroll.py:66-103 over
 // utils/model.py:193-210), as row kernels + bf16 MFMA GEMMs with population epilogues + the windowed flash kernel.
 //
-// Rows: member i's token t is row r = i * T + t of every activation; all rows of a GEMM tile belong to one member
-// (T % 128 == 0), so a member's noise row, sign and rank-1 vectors are tile-uniform. The rank-1 correction
+// Rows: member i's token t is row r = i * T + t of every activation (T % 128 == 0). The rank-1 correction
 // sign * (x . b) a^T of eggroll.py:56-58 is split between the producer of x, which writes x . b per row (or per-head /
 // per-tile partials of it), and the GEMM epilogue, which adds sign * (x . b) * a[col].
 #include <math.h>
@@ -158,111 +157,104 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// q, k = norm(rotary(q)), norm(rotary(k)) in place on the fused qkv rows (utils/model.py:55-58, 93-94). One wave per
-// row; a half-wave holds one head, lane j the rotary pair (j, j + 32).
-__global__ __launch_bounds__(256) void rope_norm_kernel(bf16_t* __restrict__ qkv, const float* __restrict__ cos_t,
-                                                        const float* __restrict__ sin_t, int T, int64_t M) {
-  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= M) return;
-  const int lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
-  const int t = (int)(r % T);
-  const float c = cos_t[t * 32 + j], s = sin_t[t * 32 + j];
-  bf16_t* row = qkv + r * kQKV;
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int head = it * 2 + half;  // 0..15 over q (0..7) and k (8..15)
-    bf16_t* hp = row + head * kHD;
-    const float x1 = bf16_to_f32(hp[j]), x2 = bf16_to_f32(hp[j + 32]);
-    const float y1 = x1 * c + x2 * s, y2 = -x1 * s + x2 * c;
-    float ss = y1 * y1 + y2 * y2;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    const float inv = rsqrtf(ss * (1.0f / kHD) + kNormEps);
-    hp[j] = f32_to_bf16(y1 * inv);
-    hp[j + 32] = f32_to_bf16(y2 * inv);
-  }
+// GEMM epilogues. The GEMM hands over one output row per wave: lane l holds columns n0 + 4l .. n0 + 4l + 3 of the
+// workgroup's 256-column tile. Noise rows are 16-byte aligned and every parameter slice starts at a multiple of 4.
+
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; }
+
+__device__ __forceinline__ void st_bf16x4(bf16_t* p, f32x4 v) {
+  const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+  const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+  *(u32x2*)p = u32x2{lo, hi};
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// out[r] = x[r, :K] . b_member (bf16 x, fp32 b); one wave per row.
-__global__ __launch_bounds__(256) void rowdot_kernel(Members mb, const bf16_t* __restrict__ x, int64_t ld, int K,
-                                                     int64_t off_b, float* __restrict__ out, int64_t M) {
-  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= M) return;
-  const int lane = threadIdx.x & 63;
-  const float* bv = mb.nrow(mb.member(r)) + off_b;
-  float d = 0.f;
-  for (int c0 = lane * 8; c0 < K; c0 += 512) {
-    const u32x4 p = *(const u32x4*)(x + r * ld + c0);
+__device__ __forceinline__ f32x4 bf16_round4(f32x4 v) {
+  f32x4 r;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      d += __uint_as_float(p[j] << 16) * bv[c0 + 2 * j] + __uint_as_float(p[j] & 0xFFFF0000u) * bv[c0 + 2 * j + 1];
-    }
-  }
-  d = warp_sum(d);
-  if (lane == 0) out[r] = d;
+  for (int k = 0; k < 4; ++k) r[k] = bf16_to_f32(f32_to_bf16(v[k]));
+  return r;
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// GEMM epilogues
-
-// qkv = h W_qkv^T + s (h . b_seg) a_seg, plus gate * (ve[tok] + s a_ve[tok] b_ve) on the v columns. A wave's 128
-// columns lie in one of the q / k / v segments. Rows are walked one 32-row MFMA tile at a time.
+// q|k|v = h W_qkv^T + s (h . b_seg) a_seg (eggroll.py:80-84); on q and k columns then the rotary embedding and the
+// per-head RMS norm (utils/model.py:55-58, 93-94: lanes l and l ^ 8 hold the rotary pairs (d, d + 32), 16 lanes a
+// head); on v columns the gated value embedding gate * (ve[tok] + s a_ve[tok] b_ve) (eggroll.py:85-89).
 struct EpiQKV {
   Members mb;
   bf16_t* out;
-  int64_t off[3];   // noise offsets of c_q, c_k, c_v
-  const float* xb;  // [M, 4]
+  int64_t off[3];     // noise offsets of c_q, c_k, c_v
+  const float* xb;    // [M, 4]
   const float* gate;  // [M, 8] or NULL
   const float* ve;    // [Vp, 512] or NULL
   int64_t off_ve;
   int Vp;
-  template <class S>
-  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*, int, int,
-                                        bool valid) const {
-    if (!valid) return;
+  const float* cos_t;  // [T, 32]
+  const float* sin_t;
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, f32x4 (&v)[R]) const {
     const int m = mb.member(row0);
     const float* nr = mb.nrow(m);
     const float s = mb.sgn(m);
-    const int seg = col0 >> 9;
-    const bool with_ve = (seg == 2) && ve;
-    float av[S::TN], bve[S::TN];
+    const int seg = n0 >> 9;
+    const int c = (n0 & (kD - 1)) + 4 * lane;
+    const int t0 = row0 - m * mb.T;
+    if (nr) {
+      const f32x4 a = ld4(nr + off[seg] + c);
+      float k[R];
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) {
-      const int c = acc_col(col0, j, lane) & (kD - 1);
-      av[j] = nr ? s * nr[off[seg] + c] : 0.f;
-      bve[j] = (with_ve && nr) ? nr[off_ve + Vp + c] : 0.f;
+      for (int q = 0; q < R; ++q) k[q] = xb[(int64_t)(row0 + q) * 4 + seg];
+#pragma unroll
+      for (int q = 0; q < R; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[q][e] += s * k[q] * a[e];
     }
+    if (seg < 2) {
+      const int j = 4 * (lane & 7);
+      const bool first = (lane & 15) < 8;
+      f32x4 cs[R], sn[R];
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i) {
+      for (int q = 0; q < R; ++q) { cs[q] = ld4(cos_t + (t0 + q) * 32 + j); sn[q] = ld4(sin_t + (t0 + q) * 32 + j); }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = acc_row(row0, i, r, lane);
-        const float xbr = nr ? xb[row * 4 + seg] : 0.f;
-        int64_t tok = 0;
-        float ate = 0.f;
-        if (with_ve) {
-          tok = mb.token(row);
-          tok = (tok < 0 || tok >= Vp) ? 0 : tok;
-          if (nr) ate = s * nr[off_ve + tok];
+      for (int q = 0; q < R; ++q) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float other = __shfl_xor(v[q][e], 8, 64);
+          v[q][e] = first ? v[q][e] * cs[q][e] + other * sn[q][e] : -other * sn[q][e] + v[q][e] * cs[q][e];
+          ss += v[q][e] * v[q][e];
         }
 #pragma unroll
-        for (int j = 0; j < S::TN; ++j) {
-          const int col = acc_col(col0, j, lane);
-          float v = acc[i][j][r] + xbr * av[j];
-          if (with_ve) {
-            const int c = col & (kD - 1);
-            v += gate[row * kH + (c >> 6)] * (ve[tok * kD + c] + ate * bve[j]);
-          }
-          out[row * kQKV + col] = f32_to_bf16(v);
-        }
+        for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float inv = rsqrtf(ss * (1.0f / kHD) + kNormEps);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[q][e] *= inv;
       }
+    } else if (ve) {
+      int64_t tok[R];
+      float g[R], at[R];
+      f32x4 e4[R];
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const int64_t tk = mb.tokens[(int64_t)mb.seq[m] * mb.T + t0 + q];
+        tok[q] = (tk < 0 || tk >= Vp) ? 0 : tk;
+      }
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        e4[q] = ld4(ve + tok[q] * kD + c);
+        g[q] = gate[(int64_t)(row0 + q) * kH + (c >> 6)];
+        at[q] = nr ? s * nr[off_ve + tok[q]] : 0.f;
+      }
+      const f32x4 b = nr ? ld4(nr + off_ve + Vp + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < R; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[q][e] += g[q] * (e4[q][e] + at[q] * b[e]);
     }
+#pragma unroll
+    for (int q = 0; q < R; ++q) st_bf16x4(out + (int64_t)(row0 + q) * kQKV + n0 + 4 * lane, v[q]);
   }
 };
 
-// x[row, col] += acc + s (sum of xb partials) a[col]   (the residual adds of utils/model.py:118-119)
+// x[row, col] += acc + s (sum of the xb partials) a[col]   (the residual adds of utils/model.py:118-119)
 struct EpiResid {
   Members mb;
   float* x;
@@ -270,34 +262,38 @@ struct EpiResid {
   int64_t off;      // noise offset of the parameter's a
   const float* xb;  // [M, nxb] partial dots, summed
   int nxb;
-  template <class S>
-  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*, int, int,
-                                        bool valid) const {
-    if (!valid) return;
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, f32x4 (&v)[R]) const {
     const int m = mb.member(row0);
     const float* nr = mb.nrow(m);
-    const float s = mb.sgn(m);
-    float av[S::TN];
+    f32x4 xv[R];
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) av[j] = nr ? s * nr[off + acc_col(col0, j, lane)] : 0.f;
+    for (int q = 0; q < R; ++q) xv[q] = ld4(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane);
+    if (nr) {
+      const float s = mb.sgn(m);
+      const f32x4 a = ld4(nr + off + n0 + 4 * lane);
+      float d[R];
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = acc_row(row0, i, r, lane);
-        float d = 0.f;
-        if (nr)
-          for (int p = 0; p < nxb; ++p) d += xb[row * nxb + p];
-#pragma unroll
-        for (int j = 0; j < S::TN; ++j) {
-          const int col = acc_col(col0, j, lane);
-          x[row * ldx + col] += acc[i][j][r] + d * av[j];
-        }
+      for (int q = 0; q < R; ++q) {
+        d[q] = 0.f;
+        for (int p = 0; p < nxb; ++p) d[q] += xb[(int64_t)(row0 + q) * nxb + p];
       }
+#pragma unroll
+      for (int q = 0; q < R; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[q][e] += s * d[q] * a[e];
+    }
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[q][e] += v[q][e];
+      *(f32x4*)(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane) = xv[q];
+    }
   }
 };
 
-// hidden = relu(acc + s (x . b) a)^2 in bf16 (utils/model.py:107)
+// hidden = relu(acc + s (x . b) a)^2 in bf16 (utils/model.py:107), and the next linear's rank-1 partial dot
+// hidden . b_next over this 256-column tile (xb_next[row, n_tile]).
 struct EpiReluSq {
   Members mb;
   bf16_t* out;
@@ -305,35 +301,49 @@ struct EpiReluSq {
   int64_t off;
   const float* xb;  // [M, xb_ld]: column 0 holds x . b
   int xb_ld;
-  template <class S>
-  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*, int, int,
-                                        bool valid) const {
-    if (!valid) return;
+  int64_t off_next_b;   // noise offset of the next linear's b (its input is this output)
+  float* xb_next;       // [M, n_tiles]
+  int n_tiles;
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, f32x4 (&v)[R]) const {
     const int m = mb.member(row0);
     const float* nr = mb.nrow(m);
-    const float s = mb.sgn(m);
-    float av[S::TN];
+    if (nr) {
+      const float s = mb.sgn(m);
+      const f32x4 a = ld4(nr + off + n0 + 4 * lane);
+      float k[R];
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) av[j] = nr ? s * nr[off + acc_col(col0, j, lane)] : 0.f;
+      for (int q = 0; q < R; ++q) k[q] = xb[(int64_t)(row0 + q) * xb_ld];
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i)
+      for (int q = 0; q < R; ++q)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = acc_row(row0, i, r, lane);
-        const float xbr = nr ? xb[row * xb_ld] : 0.f;
+        for (int e = 0; e < 4; ++e) v[q][e] += s * k[q] * a[e];
+    }
 #pragma unroll
-        for (int j = 0; j < S::TN; ++j) {
-          float v = fmaxf(acc[i][j][r] + xbr * av[j], 0.f);
-          out[row * ldo + acc_col(col0, j, lane)] = f32_to_bf16(v * v);
-        }
+    for (int q = 0; q < R; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float r = fmaxf(v[q][e], 0.f);
+        v[q][e] = r * r;
       }
+      st_bf16x4(out + (int64_t)(row0 + q) * ldo + n0 + 4 * lane, v[q]);
+    }
+    if (nr) {
+      const f32x4 b = ld4(nr + off_next_b + n0 + 4 * lane);
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const f32x4 hv = bf16_round4(v[q]);
+        float d = hv[0] * b[0] + hv[1] * b[1] + hv[2] * b[2] + hv[3] * b[3];
+        d = warp_sum(d);
+        if (lane == 0) xb_next[(int64_t)(row0 + q) * n_tiles + n_tile] = d;
+      }
+    }
   }
 };
 
-// logits z = 15 tanh((acc + s (h . b) a) / 15) (utils/model.py:203-204) and, per row of this workgroup's column
-// tile, sum over the first `vocab` columns of exp(z - 15), plus the target's logit (utils/model.py:206-209). The soft
-// cap keeps |z| < 15, so exp(z - 15) lies in (e^-30, 1]: the log-sum-exp needs no running maximum, and
-// lse = 15 + log(sum of the column-tile sums) exactly.
+// logits z = 15 tanh((acc + s (h . b) a) / 15) (utils/model.py:203-204) and, per row of this 256-column tile, the sum
+// over columns < vocab of exp(z - 15), plus the target's logit (utils/model.py:206-209). The soft cap keeps |z| < 15,
+// so exp(z - 15) lies in (e^-30, 1]: the log-sum-exp needs no running maximum, lse = 15 + log(sum of the tile sums).
 struct EpiHeadCE {
   Members mb;
   int64_t off;
@@ -344,54 +354,43 @@ struct EpiHeadCE {
   float* tgt_logit;   // [M]
   const int64_t* targets;  // [n_seq, T]
   float* logits;      // [M, vocab] or NULL
-  int64_t M;
-  template <class S>
-  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void* smem,
-                                        int m_tile, int n_tile, bool valid) const {
-    float* sm = (float*)smem;  // [WN][BM] row sums
-    const int wave = threadIdx.x >> 6, wn = wave % S::WN;
-    const int lrow0 = row0 - m_tile * S::BM;
-    if (valid) {
-      const int m = mb.member(row0);
-      const float* nr = mb.nrow(m);
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, f32x4 (&v)[R]) const {
+    const int m = mb.member(row0);
+    const float* nr = mb.nrow(m);
+    const int c0 = n0 + 4 * lane;
+    const int64_t* tgrow = targets + (int64_t)mb.seq[m] * mb.T + (row0 - m * mb.T);
+    int64_t tg[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) tg[q] = tgrow[q];
+    if (nr) {
       const float s = mb.sgn(m);
-      float av[S::TN];
+      const f32x4 a = ld4(nr + off + c0);
+      float k[R];
 #pragma unroll
-      for (int j = 0; j < S::TN; ++j) av[j] = nr ? s * nr[off + acc_col(col0, j, lane)] : 0.f;
-      const int64_t* tgrow = targets + (int64_t)mb.seq[m] * mb.T - (int64_t)m * mb.T;  // index by row
+      for (int q = 0; q < R; ++q) k[q] = xb[(int64_t)(row0 + q) * xb_ld];
 #pragma unroll
-      for (int i = 0; i < S::TM; ++i) {
+      for (int q = 0; q < R; ++q)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = acc_row(row0, i, r, lane);
-          const float xbr = nr ? xb[row * xb_ld] : 0.f;
-          const int64_t tg = tgrow[row];
-          float se = 0.f;
+        for (int e = 0; e < 4; ++e) v[q][e] += s * k[q] * a[e];
+    }
 #pragma unroll
-          for (int j = 0; j < S::TN; ++j) {
-            const int col = acc_col(col0, j, lane);
-            // 15 tanh(u / 15) = 15 - 30 / (exp(2 u / 15) + 1)
-            const float e2 = fast_exp2((acc[i][j][r] + xbr * av[j]) * (2.0f / 15.0f * kLog2e));
-            const float z = 15.0f - 30.0f * fast_rcp(e2 + 1.0f);
-            if (col < vocab) {
-              if (logits) logits[row * vocab + col] = z;
-              if (tg == col) tgt_logit[row] = z;
-              se += fast_exp2((z - 15.0f) * kLog2e);
-            }
-          }
+    for (int q = 0; q < R; ++q) {
+      const int row = row0 + q;
+      float se = 0.f;
 #pragma unroll
-          for (int o = 16; o > 0; o >>= 1) se += __shfl_xor(se, o, 64);
-          if ((lane & 31) == 0) sm[wn * S::BM + lrow0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)] = se;
+      for (int e = 0; e < 4; ++e) {
+        // 15 tanh(u / 15) = 15 - 30 / (exp(2 u / 15) + 1)
+        const float e2 = fast_exp2(v[q][e] * (2.0f / 15.0f * kLog2e));
+        const float z = 15.0f - 30.0f * fast_rcp(e2 + 1.0f);
+        if (c0 + e < vocab) {
+          se += fast_exp2((z - 15.0f) * kLog2e);
+          if (tg[q] == c0 + e) tgt_logit[row] = z;
+          if (logits) logits[(int64_t)row * vocab + c0 + e] = z;
         }
       }
-    }
-    __syncthreads();
-    for (int lr = threadIdx.x; lr < S::BM; lr += S::kThreads) {
-      const int64_t row = (int64_t)m_tile * S::BM + lr;
-      if (row >= M) continue;
-      float sum = 0.f;
-      for (int w = 0; w < S::WN; ++w) sum += sm[w * S::BM + lr];
-      part_sum[row * n_part + n_tile] = sum;
+      se = warp_sum(se);
+      if (lane == 0) part_sum[(int64_t)row * n_part + n_tile] = se;
     }
   }
 };
@@ -427,6 +426,7 @@ __global__ __launch_bounds__(256) void member_sum_kernel(const float* __restrict
 }
 
 using Tile = GemmShape<256, 256, 64, 2, 2>;
+constexpr int kAttnOG = 1;  // 32 outputs per wave (2 waves per SIMD)
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
@@ -453,7 +453,7 @@ static Workspace carve(void* base, int64_t M) {
   w.xb = (float*)take(M * 4 * 4);
   w.gate = (float*)take(M * kH * 4);
   w.xbp = (float*)take(M * kH * 4);
-  w.xb1 = (float*)take(M * 4);
+  w.xb1 = (float*)take(M * (kF / Tile::BN) * 4);
   w.psum = (float*)take(M * kHeadParts * 4);
   w.tgt = (float*)take(M * 4);
   w.row_ce = (float*)take(M * 4);
@@ -539,16 +539,10 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     }
 
     EpiQKV eq{mb, ws.qkv, {pert->c_q[i], pert->c_k[i], pert->c_v[i]}, ws.xb, L.w_gate ? ws.gate : nullptr, L.ve,
-              pert->ve[i], Vp};
+              pert->ve[i], Vp, model->rope_cos, model->rope_sin};
     {
       NoiseTimer tm(kTimeQKV, stream);
       NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_qkv, kD, (int)M, kQKV, kD, eq, stream)));
-    }
-    {
-      NoiseTimer tm(kTimeRope, stream);
-      hipLaunchKernelGGL(rope_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, ws.qkv, model->rope_cos,
-                         model->rope_sin, (int)T, M);
-      NOISE_LAUNCH_CHECK();
     }
 
     FlashArgs fa;
@@ -560,11 +554,10 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     fa.xb_vec = noisy ? pert->rows + pert->c_proj[i] + kD : nullptr;
     fa.xb_row = member_row; fa.xb_stride = pert->stride;
     fa.heads = kH; fa.T = (int)T; fa.window = L.window;
+    fa.bound = 8.0f;  // q and k are RMS-normed over 64 channels: |q . k| / 8 <= 8
     {
       NoiseTimer tm(kTimeAttention, stream);
-      hipLaunchKernelGGL(window_flash_kernel<kAttn>, dim3((unsigned)(T / kFlashBO), kH, (unsigned)members), dim3(256),
-                         0, stream, fa);
-      NOISE_LAUNCH_CHECK();
+      NOISE_CHECK_HIP((launch_flash<kAttn, true, kAttnOG>(fa, members, kH, stream)));
     }
 
     EpiResid ep{mb, ws.x, kD, pert->c_proj[i], ws.xbp, kH};
@@ -583,18 +576,12 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
       NOISE_LAUNCH_CHECK();
     }
 
-    EpiReluSq er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4};
+    EpiReluSq er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4, pert->mlp_proj[i] + kD, ws.xb1, kF / Tile::BN};
     {
       NoiseTimer tm(kTimeFc, stream);
       NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
     }
-    if (noisy) {
-      NoiseTimer tm(kTimeRowdot, stream);
-      hipLaunchKernelGGL(rowdot_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, ws.hid, (int64_t)kF, kF,
-                         pert->mlp_proj[i] + kD, ws.xb1, M);
-      NOISE_LAUNCH_CHECK();
-    }
-    EpiResid em{mb, ws.x, kD, pert->mlp_proj[i], ws.xb1, 1};
+    EpiResid em{mb, ws.x, kD, pert->mlp_proj[i], ws.xb1, kF / Tile::BN};
     {
       NoiseTimer tm(kTimeMlpProj, stream);
       NOISE_CHECK_HIP((launch_gemm<Tile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
@@ -612,7 +599,7 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
 
   const int n_part = Vp / Tile::BN;
   const int64_t* tg = targets ? targets : tokens;  // logits-only calls still run the CE bookkeeping on tokens
-  EpiHeadCE eh{mb, pert->lm_head, ws.xb, 4, model->vocab, n_part, ws.psum, ws.tgt, tg, logits, M};
+  EpiHeadCE eh{mb, pert->lm_head, ws.xb, 4, model->vocab, n_part, ws.psum, ws.tgt, tg, logits};
   {
     NoiseTimer tm(kTimeHead, stream);
     NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, model->lm_head, kD, (int)M, Vp, kD, eh, stream)));

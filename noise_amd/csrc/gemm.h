@@ -16,6 +16,8 @@
 
 namespace noise {
 
+constexpr int kEpiRows = 8;  // rows per epilogue group: consecutive, 8-aligned, so never across a member boundary
+
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct GemmShape {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
@@ -25,7 +27,10 @@ struct GemmShape {
   static constexpr int kChunks = BK / 8;              // 16-byte chunks per LDS row
   static constexpr int kAVec = BM * kChunks / kThreads;  // 16-byte global loads per thread
   static constexpr int kBVec = BN * kChunks / kThreads;
-  static constexpr int kLdsBytes = 2 * (BM + BN) * BK * 2;
+  static constexpr int kEpiLd = BN + 16;                // bf16 staging row stride (16 elements of padding)
+  static constexpr int kMainLds = 2 * (BM + BN) * BK * 2;
+  static constexpr int kEpiLds = BM * kEpiLd * 2;         // the whole tile in bf16
+  static constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(BK % 16 == 0 && kChunks <= 8 && kChunks >= 2, "BK in {16, 32, 64}");
   static_assert((BM * kChunks) % kThreads == 0 && (BN * kChunks) % kThreads == 0, "tile loads must divide threads");
@@ -140,9 +145,36 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
     }
     __syncthreads();
   }
-  // A wave tile (WTM rows) lies in one member when T % WTM == 0; past-the-end waves only join the epilogue's barriers.
-  const bool valid = m0 + wm * S::WTM < M;
-  epi.template apply<S>(acc, m0 + wm * S::WTM, n0 + wn * S::WTN, lane, (void*)smem_raw, m_tile, n_tile, valid);
+  // Epilogue through LDS. The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul
+  // output, to which it then adds its fp32 rank-1 term -- and staged as the whole 256 x 256 tile. Each wave then takes
+  // 64 rows in groups of kEpiRows (lane l holds columns 4l .. 4l+3) and hands a group to the epilogue, which issues
+  // all of the group's loads before it computes and stores. Rows past M are skipped.
+  static_assert(S::BN == 256 && S::kThreads == 256 && S::BM == 256, "row epilogue: 256 x 256 tiles, 4 waves");
+  bf16_t* st = (bf16_t*)smem_raw;
+#pragma unroll
+  for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = wm * S::WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        st[lr * S::kEpiLd + wn * S::WTN + j * 32 + (lane & 31)] = f32_to_bf16(acc[i][j][r]);
+      }
+  __syncthreads();
+  constexpr int R = kEpiRows;
+#pragma unroll 1
+  for (int g = 0; g < 64 / R; ++g) {
+    const int lr0 = wave * 64 + g * R;
+    if (m0 + lr0 >= M) break;  // M % 8 == 0: a group is all valid or all past the end
+    f32x4 v[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const u32x2 p = *(const u32x2*)(st + (lr0 + k) * S::kEpiLd + 4 * lane);
+      v[k] = f32x4{__uint_as_float(p[0] << 16), __uint_as_float(p[0] & 0xFFFF0000u), __uint_as_float(p[1] << 16),
+                   __uint_as_float(p[1] & 0xFFFF0000u)};
+    }
+    epi.template rows<R>(m0 + lr0, n0, n_tile, lane, v);
+  }
 }
 
 // Row / column of accumulator element (i, j, r) for this lane.

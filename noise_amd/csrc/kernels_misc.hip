@@ -7,7 +7,8 @@
 
 namespace noise {
 
-// y = acc + s_m u[row] a_m[col] for member m of the tile; optional fp32 store; per-tile partial sums of y^2.
+// y = acc + s_m u[row] a_m[col] for the rows' member m; optional fp32 store; per-row partial sums of y^2 over the
+// 256-column tile (part[row, n_tile]).
 struct EpiLowrank {
   int T;
   const float* noise;
@@ -16,32 +17,29 @@ struct EpiLowrank {
   const float* u;     // [M] x . b of each row
   float* y;           // [M, N] or NULL
   int64_t ldy;
-  float* part;        // [M / WTM, N / WTN] per-wave-tile partial sums of y^2, or NULL
-  template <class S>
-  __device__ __forceinline__ void apply(f32x16 (&acc)[S::TM][S::TN], int row0, int col0, int lane, void*, int, int,
-                                        bool valid) const {
-    if (!valid) return;
+  float* part;        // [M, n_tiles] or NULL
+  int n_tiles;
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, f32x4 (&v)[R]) const {
     const int m = row0 / T;
-    const float s = sign[m];
-    const float* nr = noise + (int64_t)m * stride + a_off;
-    float ss = 0.f;
+    const f32x4 a = *(const f32x4*)(noise + (int64_t)m * stride + a_off + n0 + 4 * lane);
+    float k[R];
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) {
-      const int col = acc_col(col0, j, lane);
-      const float av = s * nr[col];
+    for (int q = 0; q < R; ++q) k[q] = sign[m] * u[row0 + q];
 #pragma unroll
-      for (int i = 0; i < S::TM; ++i)
+    for (int q = 0; q < R; ++q) {
+      float ss = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = acc_row(row0, i, r, lane);
-          const float v = acc[i][j][r] + u[row] * av;
-          if (y) y[row * ldy + col] = v;
-          ss += v * v;
-        }
+      for (int e = 0; e < 4; ++e) {
+        v[q][e] += k[q] * a[e];
+        ss += v[q][e] * v[q][e];
+      }
+      if (y) *(f32x4*)(y + (int64_t)(row0 + q) * ldy + n0 + 4 * lane) = v[q];
+      if (part) {
+        ss = warp_sum(ss);
+        if (lane == 0) part[(int64_t)(row0 + q) * n_tiles + n_tile] = ss;
+      }
     }
-    if (!part) return;
-    ss = warp_sum(ss);
-    if (lane == 0) part[(int64_t)(row0 / S::WTM) * (gridDim.x * S::WN) + col0 / S::WTN] = ss;
   }
 };
 
@@ -60,15 +58,17 @@ __global__ __launch_bounds__(256) void lowrank_u_kernel(const bf16_t* __restrict
   if (lane == 0) u[r] = d;
 }
 
-// sumsq[m] = sum of the member's wave-tile partials, fixed order.
-__global__ void member_part_sum_kernel(const float* __restrict__ part, int tiles_per_member, int tiles_x,
-                                       float* __restrict__ out) {
+// sumsq[m] = sum of the member's per-row partials: one workgroup per member, fixed order (deterministic).
+__global__ __launch_bounds__(256) void member_part_sum_kernel(const float* __restrict__ part, int per_member,
+                                                              float* __restrict__ out) {
+  __shared__ float red[4];
   const int m = blockIdx.x;
-  if (threadIdx.x != 0) return;
   float s = 0.f;
-  for (int ty = 0; ty < tiles_per_member; ++ty)
-    for (int tx = 0; tx < tiles_x; ++tx) s += part[((int64_t)m * tiles_per_member + ty) * tiles_x + tx];
-  out[m] = s;
+  for (int i = threadIdx.x; i < per_member; i += 256) s += part[(int64_t)m * per_member + i];
+  s = warp_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[m] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 using LTile = GemmShape<256, 256, 64, 2, 2>;
@@ -82,7 +82,7 @@ extern "C" int noise_attention(const uint16_t* q, const uint16_t* k, const uint1
                                int64_t out_stride_b, int64_t out_stride_t, float* lse, void* stream) {
   NOISE_REQUIRE(q && k && v && out, "NULL pointer argument");
   NOISE_REQUIRE(batch > 0 && batch <= 65535 && heads > 0 && heads <= 65535, "batch / heads outside [1, 65535]");
-  NOISE_REQUIRE(T > 0 && T % kFlashBO == 0, "T = %lld must be a positive multiple of %d", (long long)T, kFlashBO);
+  NOISE_REQUIRE(T > 0 && T % 128 == 0, "T = %lld must be a positive multiple of 128", (long long)T);
   NOISE_REQUIRE(window >= 0, "negative window");
   NOISE_REQUIRE(stride_t % 8 == 0 && stride_b % 8 == 0 && out_stride_t % 4 == 0, "strides must keep 16-byte rows");
   FlashArgs a;
@@ -94,9 +94,7 @@ extern "C" int noise_attention(const uint16_t* q, const uint16_t* k, const uint1
   a.lse_out = lse;
   a.heads = heads; a.T = (int)T; a.window = window;
   NoiseTimer tm(kTimeAttention, (hipStream_t)stream);
-  hipLaunchKernelGGL(window_flash_kernel<kAttn>, dim3((unsigned)(T / kFlashBO), (unsigned)heads, (unsigned)batch),
-                     dim3(256), 0, (hipStream_t)stream, a);
-  NOISE_LAUNCH_CHECK();
+  NOISE_CHECK_HIP((launch_flash<kAttn, false, 1>(a, batch, heads, (hipStream_t)stream)));
   return NOISE_OK;
 }
 
@@ -104,7 +102,7 @@ extern "C" int noise_credit_lse(const uint16_t* q, const uint16_t* k, int64_t ro
                                 float* lse, void* stream) {
   NOISE_REQUIRE(q && k && lse, "NULL pointer argument");
   NOISE_REQUIRE(rows > 0 && rows <= 65535, "rows outside [1, 65535]");
-  NOISE_REQUIRE(T > 0 && T % kFlashBO == 0, "T = %lld must be a positive multiple of %d", (long long)T, kFlashBO);
+  NOISE_REQUIRE(T > 0 && T % 128 == 0, "T = %lld must be a positive multiple of 128", (long long)T);
   NOISE_REQUIRE(window >= 0, "negative window");
   FlashArgs a;
   memset(&a, 0, sizeof(a));
@@ -113,9 +111,7 @@ extern "C" int noise_credit_lse(const uint16_t* q, const uint16_t* k, int64_t ro
   a.lse_out = lse;
   a.heads = 1; a.T = (int)T; a.window = window;
   NoiseTimer tm(kTimeCreditLse, (hipStream_t)stream);
-  hipLaunchKernelGGL(window_flash_kernel<kLse>, dim3((unsigned)(T / kFlashBO), 1, (unsigned)rows), dim3(256), 0,
-                     (hipStream_t)stream, a);
-  NOISE_LAUNCH_CHECK();
+  NOISE_CHECK_HIP((launch_flash<kLse, false, 1>(a, rows, 1, (hipStream_t)stream)));
   return NOISE_OK;
 }
 
@@ -123,7 +119,7 @@ extern "C" int noise_credit_value(const uint16_t* q, const uint16_t* k, const fl
                                   int64_t T, int32_t window, int32_t hi_lo, float* out, void* stream) {
   NOISE_REQUIRE(q && k && lse && src && out, "NULL pointer argument");
   NOISE_REQUIRE(rows > 0 && rows <= 65535, "rows outside [1, 65535]");
-  NOISE_REQUIRE(T > 0 && T % kFlashBO == 0, "T = %lld must be a positive multiple of %d", (long long)T, kFlashBO);
+  NOISE_REQUIRE(T > 0 && T % 128 == 0, "T = %lld must be a positive multiple of 128", (long long)T);
   NOISE_REQUIRE(window >= 0, "negative window");
   FlashArgs a;
   memset(&a, 0, sizeof(a));
@@ -133,9 +129,7 @@ extern "C" int noise_credit_value(const uint16_t* q, const uint16_t* k, const fl
   a.out = out; a.o_sb = T * 64; a.o_st = 64;
   a.heads = 1; a.T = (int)T; a.window = window; a.hi_lo = hi_lo;
   NoiseTimer tm(kTimeCreditValue, (hipStream_t)stream);
-  hipLaunchKernelGGL(window_flash_kernel<kCredit>, dim3((unsigned)(T / kFlashBO), 1, (unsigned)rows), dim3(256), 0,
-                     (hipStream_t)stream, a);
-  NOISE_LAUNCH_CHECK();
+  NOISE_CHECK_HIP((launch_flash<kCredit, false, 1>(a, rows, 1, (hipStream_t)stream)));
   return NOISE_OK;
 }
 
@@ -144,8 +138,7 @@ static inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 extern "C" size_t noise_lowrank_workspace(int64_t m, int64_t T, int64_t in, int64_t out, int32_t x_shared) {
   (void)in; (void)x_shared;
   const int64_t M = m * T;
-  const int64_t tiles = ((M + LTile::BM - 1) / LTile::BM * LTile::WM) * (out / LTile::WTN);
-  return al256((size_t)M * 4) + al256((size_t)tiles * 4) + (x_shared ? al256((size_t)M * in * 2) : 0);
+  return al256((size_t)M * 4) + al256((size_t)M * (out / LTile::BN) * 4) + (x_shared ? al256((size_t)M * in * 2) : 0);
 }
 
 extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t* w, const float* noise,
@@ -165,8 +158,7 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
   float* part = (float*)((char*)workspace + al256((size_t)M * 4));
   const bf16_t* A = (const bf16_t*)x;
   if (x_shared) {  // replicate the shared operand per member (workspace), so the grouped GEMM streams one [M, in] A
-    bf16_t* rep = (bf16_t*)((char*)part + al256((size_t)((M + LTile::BM - 1) / LTile::BM * LTile::WM) *
-                                                 (out / LTile::WTN) * 4));
+    bf16_t* rep = (bf16_t*)((char*)part + al256((size_t)M * (out / LTile::BN) * 4));
     for (int64_t i = 0; i < m; ++i)
       NOISE_CHECK_HIP(hipMemcpyAsync(rep + i * T * in, x, (size_t)T * in * 2, hipMemcpyDeviceToDevice, stream));
     A = rep;
@@ -174,15 +166,15 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
   hipLaunchKernelGGL(lowrank_u_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream, A, M, (int)in, (int)T,
                      noise, noise_stride, b_off, u, M);
   NOISE_LAUNCH_CHECK();
-  EpiLowrank epi{(int)T, noise, noise_stride, a_off, sign, u, y, out, sumsq ? part : nullptr};
+  EpiLowrank epi{(int)T, noise, noise_stride, a_off, sign, u, y, out, sumsq ? part : nullptr, (int)(out / LTile::BN)};
   NOISE_CHECK_HIP((prepare_gemm<LTile, EpiLowrank>()));
   {
     NoiseTimer tm(kTimeLowrank, stream);
     NOISE_CHECK_HIP((launch_gemm<LTile>(A, in, w, in, (int)M, (int)out, (int)in, epi, stream)));
   }
   if (sumsq) {
-    hipLaunchKernelGGL(member_part_sum_kernel, dim3((unsigned)m), dim3(64), 0, stream, part, (int)(T / LTile::WTM),
-                       (int)(out / LTile::WTN), sumsq);
+    hipLaunchKernelGGL(member_part_sum_kernel, dim3((unsigned)m), dim3(256), 0, stream, part,
+                       (int)(T * (out / LTile::BN)), sumsq);
     NOISE_LAUNCH_CHECK();
   }
   return NOISE_OK;

@@ -7,12 +7,17 @@
 //   kCredit out_o = sum_i exp(x_o . y_i / 8 - lse_i) v_i over 0 <= i - o <= W  (credit value pass; x = k, y = q,
 //           v = the fp32 source as bf16 high (+ low) parts)  train/speedrun/moment_kernels.py:612-661
 //
-// A workgroup owns 128 outputs of one (batch, head) row: 4 waves x 32 outputs. Inputs stream through LDS in tiles of
-// 64. Scores are computed transposed, S^T[i, o] = y_i . x_o (v_mfma_f32_32x32x16_bf16, y from LDS as the A operand,
-// x in registers as the B operand), because the accumulator layout of S^T (lane = output column l%32, registers =
-// 16 inputs) is exactly the B-operand layout of O^T[d, o] += V^T[d, i] P^T[i, o]: the probabilities go from the
-// score registers to the value MFMA without an LDS round trip. V^T is staged transposed in LDS. Softmax statistics
-// are per lane (one output per lane, the other half of the inputs in lane ^ 32).
+// A workgroup owns 128 OG outputs of one (batch, head) row: 4 waves x OG groups of 32 outputs.
+// Inputs stream through two LDS stages in tiles of 64; the next tile's global loads are issued before the current
+// tile's MFMAs (one barrier per tile). Scores are computed transposed, S^T[i, o] = y_i . x_o (v_mfma_f32_32x32x16_bf16,
+// y from LDS as the A operand, x in registers as the B operand): the accumulator layout of S^T (lane = output l%32,
+// registers = 16 inputs) is exactly the B-operand layout of O^T[d, o] += V^T[d, i] P^T[i, o], so probabilities go
+// from score registers to the value MFMA without an LDS round trip. Every y and V^T fragment read from LDS feeds all
+// output groups of a wave. V^T is written to LDS in 8-byte chunks (4 inputs of one channel) after a 4x4 register
+// transpose; chunks are XOR-swizzled so a half-wave's reads hit distinct banks.
+//
+// kAttn with BOUNDED (a.bound > 0): the model normalizes q and k (RMS over 64 channels, so |q| = |k| <= 8 and
+// |q . k / 8| <= 8); softmax weights are then exp(s - bound) in (e^-16, ~1] with no running maximum and no rescaling.
 #pragma once
 
 #include "common.h"
@@ -35,247 +40,354 @@ struct FlashArgs {
   const int32_t* xb_row;
   int64_t xb_stride;
   int32_t heads, T, window, hi_lo;
+  float bound;          // kAttn: > 0 when |x . y / 8| <= bound is guaranteed (fixed-reference softmax)
 };
 
-constexpr int kFlashBO = 128, kFlashBI = 64;
+constexpr int kFlashBI = 64;
+template <int OG> struct FlashTile { static constexpr int BO = 4 * 32 * OG; };  // outputs per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
-
-// LDS: y tile [64][64] bf16 (8 KB), V^T hi [64][64] (8 KB), V^T lo (8 KB), lse tile [64] fp32.
-constexpr int kFlashLds = 3 * 64 * 64 * 2 + 64 * 4;
 
 __device__ __forceinline__ int vt_swz(int d, int chunk) { return chunk ^ ((d >> 1) & 15); }  // 8-byte chunks
 
 template <int MODE>
-__global__ __launch_bounds__(256) void window_flash_kernel(FlashArgs a) {
-  __shared__ __align__(16) unsigned char smem[kFlashLds];
-  bf16_t* ys = (bf16_t*)smem;
-  bf16_t* vt_hi = ys + 64 * 64;
-  bf16_t* vt_lo = vt_hi + 64 * 64;
-  float* lse_s = (float*)(vt_lo + 64 * 64);
+struct FlashStage {
+  u32x4 y[2];  // two 16-byte vectors of the y tile
+  u32x2 v[4];  // kAttn: 4 inputs x 4 channels, bf16
+  float lse;
+};
+template <>
+struct FlashStage<kCredit> {
+  u32x4 y[2];
+  f32x4 v[4];  // kCredit: 4 inputs x 4 channels, fp32
+  float lse;
+};
+
+template <int MODE, bool BOUNDED, int OG>
+__global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
+  constexpr int kBO = FlashTile<OG>::BO;
+  __shared__ __align__(16) bf16_t ys[2][64 * 64];
+  __shared__ __align__(16) bf16_t vt_hi[2][64 * 64];
+  __shared__ __align__(16) bf16_t vt_lo[MODE == kCredit ? 2 : 1][MODE == kCredit ? 64 * 64 : 4];
+  __shared__ float lse_s[2][64];
 
   const int T = a.T, W = a.window;
-  const int n_tiles = T / kFlashBO;
+  const int n_tiles = (T + kBO - 1) / kBO;
   // heaviest output tiles first (kAttn / kLse: late outputs see the most inputs; kCredit: early ones)
   const int tile = (MODE == kCredit) ? (int)blockIdx.x : n_tiles - 1 - (int)blockIdx.x;
   const int head = blockIdx.y;
   const int64_t b = blockIdx.z;
-  const int o0 = tile * kFlashBO;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int o0 = tile * kBO;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int ow = o0 + wave * 32;  // this wave's first output
-  const int my_o = ow + col;
+  const int ow = o0 + wave * 32 * OG;  // this wave's first output
+  const bool wave_live = ow < T;       // T % 128 == 0, so a live wave's outputs are all < T
 
   const bf16_t* xg = a.x + b * a.x_sb + head * 64;
   const bf16_t* yg = a.y + b * a.y_sb + head * 64;
+  constexpr bool bounded = (MODE == kAttn) && BOUNDED;
 
-  // x_o for this lane's output as four B-operand fragments (dims 16 kk + 8 half .. +7)
-  bf16x8 xf[4];
+  bf16x8 xf[OG][4];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) xf[kk] = *(const bf16x8*)(xg + (int64_t)my_o * a.x_st + kk * 16 + half * 8);
+  for (int og = 0; og < OG; ++og)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int o = wave_live ? ow + og * 32 + col : 0;
+      xf[og][kk] = *(const bf16x8*)(xg + (int64_t)o * a.x_st + kk * 16 + half * 8);
+    }
 
-  f32x16 o_acc[2];
+  f32x16 o_acc[OG][2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int og = 0; og < OG; ++og)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[t][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o_acc[og][t][r] = 0.f;
+  float m_run[OG], l_run[OG];
+#pragma unroll
+  for (int og = 0; og < OG; ++og) { m_run[og] = -INFINITY; l_run[og] = 0.f; }
   const float qk_scale = 0.125f * kLog2e;
+  const float ref = bounded ? a.bound * kLog2e : 0.f;
 
   int i_begin, i_end;  // input range of the whole workgroup [i_begin, i_end)
   if (MODE == kCredit) {
     i_begin = o0;
-    i_end = min(T, o0 + kFlashBO + W);
+    i_end = min(T, o0 + kBO + W);
   } else {
     i_begin = max(0, o0 - W);
-    i_end = o0 + kFlashBO;
+    i_end = min(T, o0 + kBO);
   }
   i_begin = i_begin / kFlashBI * kFlashBI;
 
   const float* lse_in = (MODE == kCredit) ? a.lse_in + ((int64_t)b * a.heads + head) * T : nullptr;
+  const bf16_t* vgb = (MODE == kAttn) ? (const bf16_t*)a.v + b * a.v_sb + head * 64 : nullptr;
+  const float* vgf = (MODE == kCredit) ? (const float*)a.v + b * a.v_sb + head * 64 : nullptr;
+  const int kg = tid >> 4, dg = tid & 15;  // V staging: inputs 4 kg .. 4 kg + 3, channels 4 dg .. 4 dg + 3
 
-  for (int i0 = i_begin; i0 < i_end; i0 += kFlashBI) {
-    // ---- stage y tile (swizzled rows of 8 chunks) and V^T ----
-    __syncthreads();
+  auto load = [&](int i0, FlashStage<MODE>& st) {
 #pragma unroll
     for (int rep = 0; rep < 2; ++rep) {
-      const int v = threadIdx.x + rep * 256;
+      const int v = tid + rep * 256;
+      st.y[rep] = *(const u32x4*)(yg + (int64_t)(i0 + (v >> 3)) * a.y_st + (v & 7) * 8);
+    }
+    if constexpr (MODE == kAttn) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        st.v[k] = *(const u32x2*)(vgb + (int64_t)(i0 + 4 * kg + k) * a.v_st + 4 * dg);
+      }
+    } else if constexpr (MODE == kCredit) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        st.v[k] = *(const f32x4*)(vgf + (int64_t)(i0 + 4 * kg + k) * a.v_st + 4 * dg);
+      st.lse = (tid < 64) ? lse_in[i0 + tid] : 0.f;
+    }
+  };
+  auto store = [&](int s, const FlashStage<MODE>& st) {
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+      const int v = tid + rep * 256;
       const int row = v >> 3, chunk = v & 7;
-      const u32x4 val = *(const u32x4*)(yg + (int64_t)(i0 + row) * a.y_st + chunk * 8);
-      *(u32x4*)(ys + row * 64 + ((chunk ^ (row & 7)) * 8)) = val;
+      *(u32x4*)(&ys[s][row * 64 + ((chunk ^ (row & 7)) * 8)]) = st.y[rep];
     }
-    if (MODE == kAttn) {
-      const bf16_t* vg = (const bf16_t*)a.v + b * a.v_sb + head * 64;
+    if constexpr (MODE == kAttn) {
+      // 4 inputs x 4 channels -> channel-major 8-byte chunks
 #pragma unroll
-      for (int rep = 0; rep < 2; ++rep) {
-        const int v = threadIdx.x + rep * 256;
-        const int row = v >> 3, d0 = (v & 7) * 8;  // input row, first of 8 dims
-        const u32x4 val = *(const u32x4*)(vg + (int64_t)(i0 + row) * a.v_st + d0);
-        const bf16_t* e = (const bf16_t*)&val;
+      for (int d = 0; d < 4; ++d) {
+        uint32_t e[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int d = d0 + j;
-          vt_hi[d * 64 + vt_swz(d, row >> 2) * 4 + (row & 3)] = e[j];
+        for (int k = 0; k < 4; ++k) e[k] = (st.v[k][d >> 1] >> ((d & 1) * 16)) & 0xFFFFu;
+        const int ch = 4 * dg + d;
+        *(u32x2*)(&vt_hi[s][ch * 64 + vt_swz(ch, kg) * 4]) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+      }
+    } else if constexpr (MODE == kCredit) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float f = st.v[k][d];
+          const bf16_t h = f32_to_bf16(f);
+          hi[k] = h;
+          lo[k] = f32_to_bf16(f - bf16_to_f32(h));
         }
+        const int ch = 4 * dg + d;
+        const int at = ch * 64 + vt_swz(ch, kg) * 4;
+        *(u32x2*)(&vt_hi[s][at]) = u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+        *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
       }
-    } else if (MODE == kCredit) {
-      const float* vg = (const float*)a.v + b * a.v_sb + head * 64;
-#pragma unroll
-      for (int rep = 0; rep < 4; ++rep) {
-        const int v = threadIdx.x + rep * 256;
-        const int row = v >> 4, d0 = (v & 15) * 4;
-        const f32x4 val = *(const f32x4*)(vg + (int64_t)(i0 + row) * a.v_st + d0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = d0 + j;
-          const bf16_t hi = f32_to_bf16(val[j]);
-          const int at = d * 64 + vt_swz(d, row >> 2) * 4 + (row & 3);
-          vt_hi[at] = hi;
-          vt_lo[at] = f32_to_bf16(val[j] - bf16_to_f32(hi));
-        }
-      }
-      if (threadIdx.x < 64) lse_s[threadIdx.x] = (i0 + threadIdx.x < T) ? lse_in[i0 + threadIdx.x] : 0.f;
+      if (tid < 64) lse_s[s][tid] = st.lse;
     }
-    __syncthreads();
+  };
 
-    // ---- per-wave skip of tiles with no valid pair ----
-    bool any, full;
-    if (MODE == kCredit) {
-      any = (i0 + kFlashBI - 1 >= ow) && (i0 <= ow + 31 + W);
-      full = (i0 >= ow + 31) && (i0 + kFlashBI - 1 <= ow + W);
-    } else {
-      any = (i0 <= ow + 31) && (i0 + kFlashBI - 1 >= ow - W);
-      full = (i0 + kFlashBI - 1 <= ow) && (i0 >= ow + 31 - W);
-    }
-    if (!any) continue;
+  FlashStage<MODE> stage;
+  load(i_begin, stage);
+  store(0, stage);
+  __syncthreads();
 
-    // ---- S^T = Y X^T: two 32-input tiles ----
-    f32x16 s[2];
+  int it = 0;
+  for (int i0 = i_begin; i0 < i_end; i0 += kFlashBI, ++it) {
+    const int s = it & 1;
+    const bool more = i0 + kFlashBI < i_end;
+    if (more) load(i0 + kFlashBI, stage);
+
+    // per output group: any valid pair in this tile, and no pair masked
+    bool any[OG], full[OG];
+    bool any_og = false;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
-      const int row = t * 32 + col;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 yf = *(const bf16x8*)(ys + row * 64 + (((kk * 2 + half) ^ (row & 7)) * 8));
-        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yf, xf[kk], s[t], 0, 0, 0);
+    for (int og = 0; og < OG; ++og) {
+      const int g0 = ow + og * 32;
+      if (MODE == kCredit) {
+        any[og] = wave_live && (i0 + kFlashBI - 1 >= g0) && (i0 <= g0 + 31 + W);
+        full[og] = (i0 >= g0 + 31) && (i0 + kFlashBI - 1 <= g0 + W);
+      } else {
+        any[og] = wave_live && (i0 <= g0 + 31) && (i0 + kFlashBI - 1 >= g0 - W);
+        full[og] = (i0 + kFlashBI - 1 <= g0) && (i0 >= g0 + 31 - W);
       }
+      any_og = any_og || any[og];
     }
 
-    // ---- probabilities (in place, as base-2 logits then weights) ----
-    if (MODE == kCredit) {
+    if (any_og) {
+      // ---- S^T = Y X^T for both output groups; each y fragment is read once ----
+      f32x16 sc[OG][2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int il = t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-          const int i = i0 + il;
-          const bool ok = full || ((i - my_o) >= 0 && (i - my_o) <= W && i < T);
-          const float e = s[t][r] * qk_scale - lse_s[il] * kLog2e;
-          s[t][r] = ok ? fast_exp2(e) : 0.f;
-        }
-    } else {
-      float mt = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = i0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-          const bool ok = full || ((my_o - i) >= 0 && (my_o - i) <= W);
-          const float e = ok ? s[t][r] * qk_scale : -INFINITY;
-          s[t][r] = e;
-          mt = fmaxf(mt, e);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float m_new = fmaxf(m_run, mt);
-      const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
-      const float corr = fast_exp2(m_run - m_safe);
-      float ls = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(s[t][r] - m_safe);
-          s[t][r] = p;
-          ls += p;
-        }
-      l_run = l_run * corr + ls;
-      m_run = m_new;
-      if (MODE == kAttn) {
+      for (int og = 0; og < OG; ++og)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o_acc[t][r] *= corr;
+          for (int r = 0; r < 16; ++r) sc[og][t][r] = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int row = t * 32 + col;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const bf16x8 yf = *(const bf16x8*)(&ys[s][row * 64 + (((kk * 2 + half) ^ (row & 7)) * 8)]);
+#pragma unroll
+          for (int og = 0; og < OG; ++og)
+            if (any[og]) sc[og][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yf, xf[og][kk], sc[og][t], 0, 0, 0);
+        }
+      }
+
+      // ---- probabilities ----
+#pragma unroll
+      for (int og = 0; og < OG; ++og) {
+        if (!any[og]) continue;
+        const int my_o = ow + og * 32 + col;
+        if (MODE == kCredit) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int il = t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+              const int i = i0 + il;
+              const bool ok = full[og] || ((i - my_o) >= 0 && (i - my_o) <= W);
+              const float e = fast_exp2(sc[og][t][r] * qk_scale - lse_s[s][il] * kLog2e);
+              sc[og][t][r] = ok ? e : 0.f;
+            }
+        } else if (bounded) {
+          float ls = 0.f;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int i = i0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+              const bool ok = full[og] || ((my_o - i) >= 0 && (my_o - i) <= W);
+              const float p = ok ? fast_exp2(sc[og][t][r] * qk_scale - ref) : 0.f;
+              sc[og][t][r] = p;
+              ls += p;
+            }
+          l_run[og] += ls;
+        } else {
+          float mt = -INFINITY;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int i = i0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+              const bool ok = full[og] || ((my_o - i) >= 0 && (my_o - i) <= W);
+              const float e = ok ? sc[og][t][r] * qk_scale : -INFINITY;
+              sc[og][t][r] = e;
+              mt = fmaxf(mt, e);
+            }
+          mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+          const float m_new = fmaxf(m_run[og], mt);
+          const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
+          const float corr = fast_exp2(m_run[og] - m_safe);
+          float ls = 0.f;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float p = fast_exp2(sc[og][t][r] - m_safe);
+              sc[og][t][r] = p;
+              ls += p;
+            }
+          l_run[og] = l_run[og] * corr + ls;
+          m_run[og] = m_new;
+          if (MODE == kAttn) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) o_acc[og][t][r] *= corr;
+          }
+        }
+      }
+
+      // ---- O^T += V^T P^T: 4 k-steps of 16 inputs, 2 tiles of 32 channels; V^T fragments shared by both groups ----
+      if (MODE != kLse) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int sp = 0; sp < 2; ++sp) {
+            bf16x8 pf[OG];
+#pragma unroll
+            for (int og = 0; og < OG; ++og)
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj) pf[og][jj] = (__bf16)sc[og][t][sp * 8 + jj];
+            const int base = t * 32 + sp * 16;
+            const int c0 = (base + 4 * half) >> 2, c1 = (base + 8 + 4 * half) >> 2;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) {
+              const int d = dt * 32 + col;
+              const u32x2 h0 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c0) * 4]);
+              const u32x2 h1 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c1) * 4]);
+              const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
+#pragma unroll
+              for (int og = 0; og < OG; ++og)
+                if (any[og]) o_acc[og][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[og], o_acc[og][dt], 0, 0, 0);
+              if (MODE == kCredit && a.hi_lo) {
+                const u32x2 g0 = *(const u32x2*)(&vt_lo[s][d * 64 + vt_swz(d, c0) * 4]);
+                const u32x2 g1 = *(const u32x2*)(&vt_lo[s][d * 64 + vt_swz(d, c1) * 4]);
+                const bf16x8 lf = __builtin_bit_cast(bf16x8, u32x4{g0[0], g0[1], g1[0], g1[1]});
+#pragma unroll
+                for (int og = 0; og < OG; ++og)
+                  if (any[og]) o_acc[og][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lf, pf[og], o_acc[og][dt], 0, 0, 0);
+              }
+            }
+          }
       }
     }
 
-    // ---- O^T += V^T P^T: 4 k-steps of 16 inputs, 2 tiles of 32 dims ----
-    if (MODE != kLse) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int sp = 0; sp < 2; ++sp) {
-          bf16x8 pf;
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) pf[jj] = (__bf16)s[t][sp * 8 + jj];
-          const int base = t * 32 + sp * 16;
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt) {
-            const int d = dt * 32 + col;
-            const int c0 = (base + 4 * half) >> 2, c1 = (base + 8 + 4 * half) >> 2;
-            const u32x2 lo4 = *(const u32x2*)(vt_hi + d * 64 + vt_swz(d, c0) * 4);
-            const u32x2 hi4 = *(const u32x2*)(vt_hi + d * 64 + vt_swz(d, c1) * 4);
-            const u32x4 packed = {lo4[0], lo4[1], hi4[0], hi4[1]};
-            o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, packed), pf, o_acc[dt], 0, 0, 0);
-            if (MODE == kCredit && a.hi_lo) {
-              const u32x2 l0 = *(const u32x2*)(vt_lo + d * 64 + vt_swz(d, c0) * 4);
-              const u32x2 l1 = *(const u32x2*)(vt_lo + d * 64 + vt_swz(d, c1) * 4);
-              const u32x4 pl = {l0[0], l0[1], l1[0], l1[1]};
-              o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, pl), pf, o_acc[dt], 0, 0, 0);
-            }
-          }
-        }
-    }
+    if (more) store(s ^ 1, stage);
+    __syncthreads();
   }
 
+  if (!wave_live) return;
   // ---- epilogue ----
-  if (MODE == kAttn || MODE == kLse) {
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    const float lse = (m_run + log2f(l_tot)) * (1.0f / kLog2e);
-    if (a.lse_out && half == 0) a.lse_out[((int64_t)b * a.heads + head) * T + my_o] = lse;
-    if (MODE == kAttn) {
-      const float inv = 1.0f / l_tot;
-      bf16_t* og = (bf16_t*)a.out + b * a.o_sb + (int64_t)my_o * a.o_st + head * 64;
-      float dot = 0.f;
-      const float* bv = a.xb_out ? a.xb_vec + (int64_t)a.xb_row[b] * a.xb_stride + head * 64 : nullptr;
+#pragma unroll
+  for (int og = 0; og < OG; ++og) {
+    const int my_o = ow + og * 32 + col;
+    if (MODE == kAttn || MODE == kLse) {
+      const float l_tot = l_run[og] + __shfl_xor(l_run[og], 32, 64);
+      const float mref = bounded ? ref : m_run[og];
+      const float lse = (mref + log2f(l_tot)) * (1.0f / kLog2e);
+      if (a.lse_out && half == 0) a.lse_out[((int64_t)b * a.heads + head) * T + my_o] = lse;
+      if (MODE == kAttn) {
+        const float inv = 1.0f / l_tot;
+        bf16_t* og_ptr = (bf16_t*)a.out + b * a.o_sb + (int64_t)my_o * a.o_st + head * 64;
+        float dot = 0.f;
+        const float* bv = a.xb_out ? a.xb_vec + (int64_t)a.xb_row[b] * a.xb_stride + head * 64 : nullptr;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d = dt * 32 + g * 8 + half * 4;
+            bf16_t e[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              e[j] = f32_to_bf16(o_acc[og][dt][g * 4 + j] * inv);
+              if (bv) dot += bf16_to_f32(e[j]) * bv[d + j];
+            }
+            *(u32x2*)(og_ptr + d) = u32x2{(uint32_t)e[0] | ((uint32_t)e[1] << 16), (uint32_t)e[2] | ((uint32_t)e[3] << 16)};
+          }
+        if (a.xb_out) {
+          dot += __shfl_xor(dot, 32, 64);
+          if (half == 0) a.xb_out[(b * T + my_o) * a.heads + head] = dot;
+        }
+      }
+    } else {
+      float* og_ptr = (float*)a.out + b * a.o_sb + (int64_t)my_o * a.o_st + head * 64;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = dt * 32 + g * 8 + half * 4;
-          bf16_t e[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            e[j] = f32_to_bf16(o_acc[dt][g * 4 + j] * inv);
-            if (bv) dot += bf16_to_f32(e[j]) * bv[d + j];
-          }
-          *(u32x2*)(og + d) = u32x2{(uint32_t)e[0] | ((uint32_t)e[1] << 16), (uint32_t)e[2] | ((uint32_t)e[3] << 16)};
+          *(f32x4*)(og_ptr + d) =
+              f32x4{o_acc[og][dt][g * 4], o_acc[og][dt][g * 4 + 1], o_acc[og][dt][g * 4 + 2], o_acc[og][dt][g * 4 + 3]};
         }
-      if (a.xb_out) {
-        dot += __shfl_xor(dot, 32, 64);
-        if (half == 0) a.xb_out[(b * T + my_o) * a.heads + head] = dot;
-      }
     }
-  } else {
-    float* og = (float*)a.out + b * a.o_sb + (int64_t)my_o * a.o_st + head * 64;
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = dt * 32 + g * 8 + half * 4;
-        *(f32x4*)(og + d) = f32x4{o_acc[dt][g * 4], o_acc[dt][g * 4 + 1], o_acc[dt][g * 4 + 2], o_acc[dt][g * 4 + 3]};
-      }
   }
+}
+
+}  // namespace noise
+
+namespace noise {
+
+// One launch of the flash kernel over `batch` x `heads` rows of T tokens (T % 128 == 0).
+template <int MODE, bool BOUNDED, int OG>
+inline hipError_t launch_flash(const FlashArgs& a, int64_t batch, int heads, hipStream_t stream) {
+  constexpr int kBO = FlashTile<OG>::BO;
+  hipLaunchKernelGGL((window_flash_kernel<MODE, BOUNDED, OG>), dim3((unsigned)((a.T + kBO - 1) / kBO), (unsigned)heads,
+                     (unsigned)batch), dim3(256), 0, stream, a);
+  return hipGetLastError();
 }
 
 }  // namespace noise
