@@ -88,7 +88,10 @@ def roofline_from_timing(timing, flops):
         tf = f / (avg_ms * 1e-3) / 1e12
         kernels[name] = dict(launches=n, avg_ms=round(avg_ms, 4), total_ms=round(ms, 3), tflops=round(tf, 1),
                              frac=round(tf / PEAK_BF16_TFLOPS, 4))
-    dom = max(kernels, key=lambda k: kernels[k]['total_ms'])
+    for name, (n, ms) in timing.items():
+        if n and name not in kernels:
+            kernels[name] = dict(launches=n, avg_ms=round(ms / n, 4), total_ms=round(ms, 3))
+    dom = max(flops.keys() & kernels.keys(), key=lambda k: kernels[k]['total_ms'])
     k = kernels[dom]
     roof = dict(bound='mfma', kernel=dom, achieved=k['tflops'], peak=PEAK_BF16_TFLOPS, unit='TFLOP/s', frac=k['frac'],
                 traffic=None, flop_per_launch=flops[dom], avg_launch_ms=k['avg_ms'])

@@ -38,6 +38,29 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
+// Sums of 8 per-lane values over the 64 lanes, by a transposed butterfly (10 shuffles instead of 8 x 6): returns
+// the total of value (4 b5 + 2 b4 + b3) where b5 b4 b3 are bits 5..3 of the lane id (8 lanes hold each total).
+__device__ __forceinline__ float warp_sum8(const float (&p)[8], int lane) {
+  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+  float q[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float send = b5 ? p[r] : p[r + 4];
+    q[r] = (b5 ? p[r + 4] : p[r]) + __shfl_xor(send, 32, 64);
+  }
+  float w[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const float send = b4 ? q[r] : q[r + 2];
+    w[r] = (b4 ? q[r + 2] : q[r]) + __shfl_xor(send, 16, 64);
+  }
+  float z = (b3 ? w[1] : w[0]) + __shfl_xor(b3 ? w[0] : w[1], 8, 64);
+  z += __shfl_xor(z, 4, 64);
+  z += __shfl_xor(z, 2, 64);
+  z += __shfl_xor(z, 1, 64);
+  return z;
+}
+
 __device__ __forceinline__ float warp_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

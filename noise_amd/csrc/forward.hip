@@ -329,14 +329,16 @@ struct EpiReluSq {
       st_bf16x4(out + (int64_t)(row0 + q) * ldo + n0 + 4 * lane, v[q]);
     }
     if (nr) {
+      static_assert(R == 8, "warp_sum8 reduces 8 rows");
       const f32x4 b = ld4(nr + off_next_b + n0 + 4 * lane);
+      float d[R];
 #pragma unroll
       for (int q = 0; q < R; ++q) {
         const f32x4 hv = bf16_round4(v[q]);
-        float d = hv[0] * b[0] + hv[1] * b[1] + hv[2] * b[2] + hv[3] * b[3];
-        d = warp_sum(d);
-        if (lane == 0) xb_next[(int64_t)(row0 + q) * n_tiles + n_tile] = d;
+        d[q] = hv[0] * b[0] + hv[1] * b[1] + hv[2] * b[2] + hv[3] * b[3];
       }
+      const float tot = warp_sum8(d, lane);
+      if ((lane & 7) == 0) xb_next[(int64_t)(row0 + (lane >> 3)) * n_tiles + n_tile] = tot;
     }
   }
 };
@@ -374,24 +376,26 @@ struct EpiHeadCE {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[q][e] += s * k[q] * a[e];
     }
+    static_assert(R == 8, "warp_sum8 reduces 8 rows");
+    float se[R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
       const int row = row0 + q;
-      float se = 0.f;
+      se[q] = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         // 15 tanh(u / 15) = 15 - 30 / (exp(2 u / 15) + 1)
         const float e2 = fast_exp2(v[q][e] * (2.0f / 15.0f * kLog2e));
         const float z = 15.0f - 30.0f * fast_rcp(e2 + 1.0f);
         if (c0 + e < vocab) {
-          se += fast_exp2((z - 15.0f) * kLog2e);
+          se[q] += fast_exp2((z - 15.0f) * kLog2e);
           if (tg[q] == c0 + e) tgt_logit[row] = z;
           if (logits) logits[(int64_t)row * vocab + c0 + e] = z;
         }
       }
-      se = warp_sum(se);
-      if (lane == 0) part_sum[(int64_t)row * n_part + n_tile] = se;
     }
+    const float tot = warp_sum8(se, lane);
+    if ((lane & 7) == 0) part_sum[(int64_t)(row0 + (lane >> 3)) * n_part + n_tile] = tot;
   }
 };
 

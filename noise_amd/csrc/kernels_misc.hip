@@ -23,22 +23,23 @@ struct EpiLowrank {
   __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, f32x4 (&v)[R]) const {
     const int m = row0 / T;
     const f32x4 a = *(const f32x4*)(noise + (int64_t)m * stride + a_off + n0 + 4 * lane);
-    float k[R];
+    static_assert(R == 8, "warp_sum8 reduces 8 rows");
+    float k[R], ss[R];
 #pragma unroll
     for (int q = 0; q < R; ++q) k[q] = sign[m] * u[row0 + q];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      float ss = 0.f;
+      ss[q] = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[q][e] += k[q] * a[e];
-        ss += v[q][e] * v[q][e];
+        ss[q] += v[q][e] * v[q][e];
       }
       if (y) *(f32x4*)(y + (int64_t)(row0 + q) * ldy + n0 + 4 * lane) = v[q];
-      if (part) {
-        ss = warp_sum(ss);
-        if (lane == 0) part[(int64_t)(row0 + q) * n_tiles + n_tile] = ss;
-      }
+    }
+    if (part) {
+      const float tot = warp_sum8(ss, lane);
+      if ((lane & 7) == 0) part[(int64_t)(row0 + (lane >> 3)) * n_tiles + n_tile] = tot;
     }
   }
 };
