@@ -82,11 +82,16 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   constexpr int kStage = (S::BM + S::BN) * S::BK;
 
   // Workgroups are dispatched round-robin over the 8 XCDs; tiles are renumbered so that each XCD walks a contiguous
-  // run of tiles in row-panel order (the A panel of a row tile is then fetched into one XCD's L2).
-  const int nt = gridDim.x, total = gridDim.x * gridDim.y;
+  // run of tiles (its A panels and B tiles are then fetched into one XCD's L2).
+  // Within a run, tiles go in groups of up to 8 row panels with the column tiles outermost, so a B tile is reused
+  // by 8 row panels while they are resident (the 4 MB lm_head weight does not fit one L2 next to its A panels).
+  const int nt = gridDim.x, mt = gridDim.y, total = nt * mt;
   const int bid = blockIdx.y * nt + blockIdx.x;
   const int tile = (total % 8 == 0) ? (bid % 8) * (total / 8) + bid / 8 : bid;
-  const int m_tile = tile / nt, n_tile = tile % nt;
+  constexpr int kGroup = 8;
+  const int grp = tile / (kGroup * nt), in_grp = tile % (kGroup * nt);
+  const int grp_rows = min(kGroup, mt - grp * kGroup);
+  const int m_tile = grp * kGroup + in_grp % grp_rows, n_tile = in_grp / grp_rows;
   const int m0 = m_tile * S::BM, n0 = n_tile * S::BN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / S::WN, wn = wave % S::WN;

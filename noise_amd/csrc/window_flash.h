@@ -72,10 +72,24 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
 
   const int T = a.T, W = a.window;
   const int n_tiles = (T + kBO - 1) / kBO;
+  // Workgroups go round-robin to the 8 XCDs. When the (batch, head) rows divide by 8, XCD x takes rows x, x + 8, ...
+  // and runs every output tile of a row back to back, so the row's inputs (512 KB at T = 2048) stay in its L2.
+  const int64_t n_rows = (int64_t)gridDim.y * gridDim.z;
+  const int64_t bid = blockIdx.x + (int64_t)n_tiles * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  int64_t row_idx;
+  int tile_idx;
+  if (n_rows % 8 == 0) {
+    const int64_t slot = bid >> 3;
+    row_idx = (bid & 7) + 8 * (slot / n_tiles);
+    tile_idx = (int)(slot % n_tiles);
+  } else {
+    row_idx = bid / n_tiles;
+    tile_idx = (int)(bid % n_tiles);
+  }
   // heaviest output tiles first (kAttn / kLse: late outputs see the most inputs; kCredit: early ones)
-  const int tile = (MODE == kCredit) ? (int)blockIdx.x : n_tiles - 1 - (int)blockIdx.x;
-  const int head = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  const int tile = (MODE == kCredit) ? tile_idx : n_tiles - 1 - tile_idx;
+  const int head = (int)(row_idx % gridDim.y);
+  const int64_t b = row_idx / gridDim.y;
   const int o0 = tile * kBO;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
