@@ -3,14 +3,16 @@
 // is where the population-specific work (rank-1 member corrections, residual adds, relu^2, soft-capped CE) happens.
 //
 // Tiling: a workgroup computes BM x BN with WM x WN waves; a wave owns (BM/WM) x (BN/WN) as 32x32 MFMA tiles
-// (v_mfma_f32_32x32x16_bf16). K advances in BK steps through two LDS buffers: the next tile's global loads are
-// issued before the current tile's MFMAs, and stored to the other buffer after them (one barrier per step).
-// LDS rows are BK bf16 = BK/8 16-byte chunks; chunk c of row r is stored at c ^ (r & 7), so the 8 rows a
-// ds_read_b128 phase touches fall on distinct banks.
+// (v_mfma_f32_32x32x16_bf16). K advances in BK steps through two LDS buffers: the next step's buffer loads are issued
+// before the current step's MFMAs and stored to the other buffer after them (one barrier per step).
+// LDS rows are BK bf16 = BK/8 16-byte chunks, XOR-swizzled (swz below) so that every ds_read_b128 / ds_write_b128
+// phase is free of bank conflicts.
 //
 // MFMA 32x32x16 bf16 lane layout (checked on gfx950): lane l supplies A[row l%32][k 8(l/32)..8(l/32)+7] and
 // B^T[col l%32][same k]; accumulator register r holds C[row (r/4)*8 + (l/32)*4 + r%4][col l%32].
 #pragma once
+
+#include <type_traits>
 
 #include "common.h"
 
@@ -36,55 +38,28 @@ struct GemmShape {
   static_assert((BM * kChunks) % kThreads == 0 && (BN * kChunks) % kThreads == 0, "tile loads must divide threads");
 };
 
+// 16-byte chunk c of LDS row r is stored at c ^ ((r >> 1) & (kChunks - 1)): a ds_read_b128 / ds_write_b128 phase
+// (16 lanes, 256 bytes) then touches 16 distinct bank groups both for fragment reads (16 consecutive rows, one chunk)
+// and for tile stores (2 rows x 8 chunks).
 template <int kChunks>
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return chunk ^ (row & (kChunks - 1));
-}
-
-// Row-major [rows x BK] bf16 tile of a K-contiguous matrix -> registers (16 bytes per vector).
-template <class S, int kVec>
-__device__ __forceinline__ void load_tile(const bf16_t* __restrict__ g, int64_t ld, int row0, int rows_valid, int k0,
-                                          u32x4 (&r)[kVec]) {
-#pragma unroll
-  for (int i = 0; i < kVec; ++i) {
-    const int v = threadIdx.x + i * S::kThreads;
-    const int row = v / S::kChunks, chunk = v % S::kChunks;
-    if (row < rows_valid)
-      r[i] = *(const u32x4*)(g + (int64_t)(row0 + row) * ld + k0 + chunk * 8);
-    else
-      r[i] = u32x4{0u, 0u, 0u, 0u};
-  }
-}
-
-template <class S, int kVec>
-__device__ __forceinline__ void store_tile(bf16_t* lds, const u32x4 (&r)[kVec]) {
-#pragma unroll
-  for (int i = 0; i < kVec; ++i) {
-    const int v = threadIdx.x + i * S::kThreads;
-    const int row = v / S::kChunks, chunk = v % S::kChunks;
-    *(u32x4*)(lds + row * S::BK + swz<S::kChunks>(row, chunk) * 8) = r[i];
-  }
-}
-
-template <class S>
-__device__ __forceinline__ bf16x8 read_frag(const bf16_t* lds, int row, int kchunk) {
-  return *(const bf16x8*)(lds + row * S::BK + swz<S::kChunks>(row, kchunk) * 8);
+  return chunk ^ ((row >> 1) & (kChunks - 1));
 }
 
 template <class S, class Epi>
 __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __restrict__ A, int64_t lda,
                                                               const bf16_t* __restrict__ B, int64_t ldb, int M, int N,
                                                               int K, Epi epi) {
+  static_assert(S::BK == 64, "main loop: 8 chunks of 16 bytes per LDS row");
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  // stage s: A tile at lds + s * kStage, B tile at lds + s * kStage + BM * BK (offsets, not a pointer array, so the
-  // accesses stay ds_read / ds_write)
-  bf16_t* lds = (bf16_t*)smem_raw;
-  constexpr int kStage = (S::BM + S::BN) * S::BK;
+  // LDS (bytes): A stage s at s * kAStage, B stage s at 2 * kAStage + s * kBStage. Every LDS access below is a
+  // per-lane base register plus an immediate offset (< 64 KB).
+  constexpr int kAStage = S::BM * S::BK * 2, kBStage = S::BN * S::BK * 2;
 
   // Workgroups are dispatched round-robin over the 8 XCDs; tiles are renumbered so that each XCD walks a contiguous
-  // run of tiles (its A panels and B tiles are then fetched into one XCD's L2).
-  // Within a run, tiles go in groups of up to 8 row panels with the column tiles outermost, so a B tile is reused
-  // by 8 row panels while they are resident (the 4 MB lm_head weight does not fit one L2 next to its A panels).
+  // run of tiles (its A panels and B tiles are then fetched into one XCD's L2). Within a run, tiles go in groups of
+  // up to 8 row panels with the column tiles outermost, so a B tile is reused by 8 row panels while they are
+  // resident (the 4 MB lm_head weight does not fit one L2 next to its A panels).
   const int nt = gridDim.x, mt = gridDim.y, total = nt * mt;
   const int bid = blockIdx.y * nt + blockIdx.x;
   const int tile = (total % 8 == 0) ? (bid % 8) * (total / 8) + bid / 8 : bid;
@@ -97,6 +72,28 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   const int wm = wave / S::WN, wn = wave % S::WN;
   const int a_rows = min(S::BM, M - m0), b_rows = min(S::BN, N - n0);
 
+  // Buffer resources over this tile's rows: reads past the last row return zeros. The K step and the row pass go
+  // in the scalar offset, so a load costs no vector address arithmetic.
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(A + (int64_t)m0 * lda), 0, a_rows * (int)lda * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(B + (int64_t)n0 * ldb), 0, b_rows * (int)ldb * 2, 0x00020000);
+  constexpr int kRowsPerPass = S::kThreads / S::kChunks;  // rows covered by one 16-byte load per thread
+  const int lrow = threadIdx.x / S::kChunks, lchunk = threadIdx.x % S::kChunks;
+  const int a_voff = (lrow * (int)lda + lchunk * 8) * 2, b_voff = (lrow * (int)ldb + lchunk * 8) * 2;
+  const int a_pass = kRowsPerPass * (int)lda * 2, b_pass = kRowsPerPass * (int)ldb * 2;
+  const int st_off = (lrow * S::BK + swz<S::kChunks>(lrow, lchunk) * 8) * 2;  // rows lrow + 32 i share the swizzle
+
+  // fragment offsets for each 16-deep k-substep (row bits 1..3 = lane bits 1..3)
+  const int xs = ((lane & 31) >> 1) & 7;
+  int fa_off[S::BK / 16], fb_off[S::BK / 16];
+#pragma unroll
+  for (int kk = 0; kk < S::BK / 16; ++kk) {
+    const int ch = ((2 * kk + (lane >> 5)) ^ xs) * 16;
+    fa_off[kk] = (wm * S::WTM + (lane & 31)) * S::BK * 2 + ch;
+    fb_off[kk] = 2 * kAStage + (wn * S::WTN + (lane & 31)) * S::BK * 2 + ch;
+  }
+
   f32x16 acc[S::TM][S::TN];
 #pragma unroll
   for (int i = 0; i < S::TM; ++i)
@@ -106,37 +103,48 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   u32x4 ra[S::kAVec], rb[S::kBVec];
-  load_tile<S, S::kAVec>(A, lda, m0, a_rows, 0, ra);
-  load_tile<S, S::kBVec>(B, ldb, n0, b_rows, 0, rb);
-  store_tile<S, S::kAVec>(lds, ra);
-  store_tile<S, S::kBVec>(lds + S::BM * S::BK, rb);
-  __syncthreads();
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < S::kAVec; ++i)
+      ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, i * a_pass + kt * S::BK * 2, 0));
+#pragma unroll
+    for (int i = 0; i < S::kBVec; ++i)
+      rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, b_voff, i * b_pass + kt * S::BK * 2, 0));
+  };
+  auto lstore = [&](int stage) {
+    const int sa = stage * kAStage, sb = 2 * kAStage + stage * kBStage;
+#pragma unroll
+    for (int i = 0; i < S::kAVec; ++i) *(u32x4*)(smem_raw + sa + st_off + i * kRowsPerPass * S::BK * 2) = ra[i];
+#pragma unroll
+    for (int i = 0; i < S::kBVec; ++i) *(u32x4*)(smem_raw + sb + st_off + i * kRowsPerPass * S::BK * 2) = rb[i];
+  };
+  auto frag = [&](int off) { return *(const bf16x8*)(smem_raw + off); };
 
   const int nk = K / S::BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  // K steps on LDS stage P = kt & 1: issue the next step's loads, run the MFMAs (fragments of k-substep kk + 1 are
+  // read while those of kk multiply), store the loaded step to stage P ^ 1, barrier
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      load_tile<S, S::kAVec>(A, lda, m0, a_rows, (kt + 1) * S::BK, ra);
-      load_tile<S, S::kBVec>(B, ldb, n0, b_rows, (kt + 1) * S::BK, rb);
-    }
-    const bf16_t* as = lds + cur * kStage;
-    const bf16_t* bs = as + S::BM * S::BK;
-    // fragments of k-substep kk + 1 are read while the MFMAs of kk run
+    const int P = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) gload(kt + 1);
+    const int pa = P * kAStage, pb = P * kBStage;
     bf16x8 fa[2][S::TM], fb[2][S::TN];
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i) fa[0][i] = read_frag<S>(as, wm * S::WTM + i * 32 + (lane & 31), (lane >> 5));
+    for (int i = 0; i < S::TM; ++i) fa[0][i] = frag(fa_off[0] + pa + i * 32 * S::BK * 2);
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) fb[0][j] = read_frag<S>(bs, wn * S::WTN + j * 32 + (lane & 31), (lane >> 5));
+    for (int j = 0; j < S::TN; ++j) fb[0][j] = frag(fb_off[0] + pb + j * 32 * S::BK * 2);
 #pragma unroll
     for (int kk = 0; kk < S::BK / 16; ++kk) {
       const int c = kk & 1;
       if (kk + 1 < S::BK / 16) {
 #pragma unroll
-        for (int i = 0; i < S::TM; ++i)
-          fa[c ^ 1][i] = read_frag<S>(as, wm * S::WTM + i * 32 + (lane & 31), (kk + 1) * 2 + (lane >> 5));
+        for (int i = 0; i < S::TM; ++i) fa[c ^ 1][i] = frag(fa_off[kk + 1] + pa + i * 32 * S::BK * 2);
 #pragma unroll
-        for (int j = 0; j < S::TN; ++j)
-          fb[c ^ 1][j] = read_frag<S>(bs, wn * S::WTN + j * 32 + (lane & 31), (kk + 1) * 2 + (lane >> 5));
+        for (int j = 0; j < S::TN; ++j) fb[c ^ 1][j] = frag(fb_off[kk + 1] + pb + j * 32 * S::BK * 2);
       }
 #pragma unroll
       for (int i = 0; i < S::TM; ++i)
@@ -144,12 +152,10 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
         for (int j = 0; j < S::TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][i], fb[c][j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) {
-      store_tile<S, S::kAVec>(lds + (cur ^ 1) * kStage, ra);
-      store_tile<S, S::kBVec>(lds + (cur ^ 1) * kStage + S::BM * S::BK, rb);
-    }
+    if (more) lstore(P ^ 1);
     __syncthreads();
   }
+
   // Epilogue through LDS. The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul
   // output, to which it then adds its fp32 rank-1 term -- and staged as the whole 256 x 256 tile. Each wave then takes
   // 64 rows in groups of kEpiRows (lane l holds columns 4l .. 4l+3) and hands a group to the epilogue, which issues

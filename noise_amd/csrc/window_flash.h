@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
     for (int rep = 0; rep < 2; ++rep) {
       const int v = tid + rep * 256;
       const int row = v >> 3, chunk = v & 7;
-      *(u32x4*)(&ys[s][row * 64 + ((chunk ^ (row & 7)) * 8)]) = st.y[rep];
+      *(u32x4*)(&ys[s][row * 64 + ((chunk ^ ((row >> 1) & 7)) * 8)]) = st.y[rep];
     }
     if constexpr (MODE == kAttn) {
       // 4 inputs x 4 channels -> channel-major 8-byte chunks
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
         const int row = t * 32 + col;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8 yf = *(const bf16x8*)(&ys[s][row * 64 + (((kk * 2 + half) ^ (row & 7)) * 8)]);
+          const bf16x8 yf = *(const bf16x8*)(&ys[s][row * 64 + (((kk * 2 + half) ^ ((row >> 1) & 7)) * 8)]);
 #pragma unroll
           for (int og = 0; og < OG; ++og)
             if (any[og]) sc[og][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yf, xf[og][kk], sc[og][t], 0, 0, 0);
