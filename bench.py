@@ -2,6 +2,7 @@
 """Benchmark of the population hot path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--workload c4|c5] [--no-cpu-baseline] [--no-credit]
+    python bench.py --copy-calibration      # one plain 1 GiB device copy, to scale rocprofv3 FETCH/WRITE_SIZE
 
 A step is one pass of the hot path over one batch of synthetic input:
   c4 (default): the 8-layer population forward of BASELINE config 4: 256 antithetic members (128 pairs), each
@@ -11,7 +12,9 @@ A step is one pass of the hot path over one batch of synthetic input:
       512 members, fitness, outer-product gradient assembly and AdamW. 50,331,648 member-tokens.
 The JSON line carries the metric of BASELINE.json, the roofline of the dominant kernel (HIP events on the launch
 stream over the timed region), the oracle's CPU throughput on a bounded sample, and the credit readout's TFLOP/s at
-config 3 (B16 H8 T2048 d64).
+config 3 (B16 H8 T2048 d64). `roofline.traffic` is the dominant kernel's HBM bytes per launch as recorded in
+profiles/population_forward_c4_traffic.txt (rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this script, each scaled
+by what the counter reads for --copy-calibration); it is null for a workload or kernel that file does not cover.
 """
 from __future__ import annotations
 
@@ -78,7 +81,23 @@ def kernel_flops(n_eval, T, windows, n_layer):
     }
 
 
-def roofline_from_timing(timing, flops):
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'population_forward_c4_traffic.txt')
+
+
+def load_traffic(path=TRAFFIC_FILE):
+    """Per-class HBM bytes per launch from the committed rocprofv3 summary: lines `traffic <class> <bytes> ...`."""
+    out = {}
+    if not os.path.exists(path):
+        return out
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 3 and parts[0] == 'traffic':
+                out[parts[1]] = int(parts[2])
+    return out
+
+
+def roofline_from_timing(timing, flops, traffic=None):
     kernels = {}
     for name, f in flops.items():
         n, ms = timing.get(name, (0, 0.0))
@@ -94,7 +113,10 @@ def roofline_from_timing(timing, flops):
     dom = max(flops.keys() & kernels.keys(), key=lambda k: kernels[k]['total_ms'])
     k = kernels[dom]
     roof = dict(bound='mfma', kernel=dom, achieved=k['tflops'], peak=PEAK_BF16_TFLOPS, unit='TFLOP/s', frac=k['frac'],
-                traffic=None, flop_per_launch=flops[dom], avg_launch_ms=k['avg_ms'])
+                traffic=(traffic or {}).get(dom), flop_per_launch=flops[dom], avg_launch_ms=k['avg_ms'])
+    if roof['traffic'] is not None:
+        roof['traffic_source'] = 'profiles/' + os.path.basename(TRAFFIC_FILE)
+        roof['traffic_gbs'] = round(roof['traffic'] / (k['avg_ms'] * 1e-3) / 1e9, 1)
     return roof, kernels
 
 
@@ -138,7 +160,8 @@ def bench_c4(args, dev):
     finite = bool(torch.isfinite(losses).all().item())
     member_tokens = members * n_seq * T_SEQ
     windows = [w for w, _ in model.window_sizes]
-    roof, kernels = roofline_from_timing(timing, kernel_flops(members * n_seq, T_SEQ, windows, len(windows)))
+    roof, kernels = roofline_from_timing(timing, kernel_flops(members * n_seq, T_SEQ, windows, len(windows)),
+                                         load_traffic())
     res = dict(value=member_tokens * args.steps / dt, ms_per_step=dt / args.steps * 1e3, member_tokens=member_tokens,
                roofline=roof, kernels=kernels, finite=finite,
                mean_member_ce=float(losses.mean().item() / (n_seq * T_SEQ)),
@@ -245,6 +268,17 @@ def cpu_baseline(model, sample_members=4, T=T_SEQ, reps=3):
                 f'({med:.2f} s each)')
 
 
+def copy_calibration(dev, nbytes=1 << 30):
+    """One device-to-device copy of `nbytes`: reads and writes exactly nbytes of HBM."""
+    import torch
+    a = torch.ones(nbytes // 4, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(copy_calibration_bytes=nbytes)), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
@@ -253,6 +287,8 @@ def main():
     ap.add_argument('--workload', choices=['c4', 'c5'], default='c4')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-credit', action='store_true')
+    ap.add_argument('--copy-calibration', action='store_true',
+                    help='run one plain device copy of exactly 1 GiB and exit (rocprofv3 counter calibration)')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         sys.exit('bench.py measures one GPU: this build runs the hot path on a single MI355X; '
@@ -262,6 +298,9 @@ def main():
     _lib.lib()
     dev = torch.device('cuda', 0)
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return
     res = bench_c4(args, dev) if args.workload == 'c4' else bench_c5(args, dev)
     model = res.pop('model')
     line = dict(metric=METRIC, value=round(res['value'], 1), unit='member-tokens/s', n_gpus=1, steps=args.steps,
