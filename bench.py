@@ -209,7 +209,8 @@ def bench_c5(args, dev):
 
 
 def bench_credit(dev, iters=10):
-    """Config 3: lse + value pass, B16 H8 T2048 d64, Q/K bf16 N(0,1)/8, E N(0,1) fp32, full causal window."""
+    """Config 3: lse + value pass, B16 H8 T2048 d64, Q/K bf16 N(0,1)/8, E N(0,1) fp32, full causal window and 1024;
+    also the key-context pass (lse and center) on the same q / k with bf16 values and hub."""
     import torch
     from noise_amd import _lib, credit
     rows, T = 16 * 8, 2048
@@ -238,6 +239,21 @@ def bench_credit(dev, iters=10):
             frac=round(flops / ((lse_ms + val_ms) * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             lse_ms=round(lse_ms, 4), value_ms=round(val_ms, 4),
             value_pass_tflops=round(4 * 64 * npairs / (val_ms * 1e-3) / 1e12, 1))
+        # the key-context pass (lse and center): q.k and hub.v dots, 4d FLOPs per pair
+        vals = (torch.randn(rows, T, 64, device=dev, generator=g)).bfloat16()
+        hub = e.bfloat16()
+        for _ in range(2):
+            credit.key_context(q, k, vals, hub, window)
+        torch.cuda.synchronize()
+        _lib.timing_enable(True)
+        for _ in range(iters):
+            credit.key_context(q, k, vals, hub, window)
+        torch.cuda.synchronize()
+        tm = _lib.timing_read()
+        _lib.timing_enable(False)
+        ctx_ms = tm['credit_center'][1] / tm['credit_center'][0]
+        out[f'window_{window}'].update(key_context_ms=round(ctx_ms, 4),
+                                       key_context_tflops=round(4 * 64 * npairs / (ctx_ms * 1e-3) / 1e12, 1))
     out['headline'] = f"{out[f'window_{T}']['tflops']} TFLOP/s at 6d per causal pair ({pairs:,} pairs)"
     return out
 

@@ -68,7 +68,7 @@ size_t noise_lowrank_workspace(int64_t m, int64_t T, int64_t in, int64_t out, in
 /* ---- a5: windowed causal attention ------------------------------------------------------------------------ */
 
 /* out[b, t, h, :] = softmax_s(q[b,t,h] . k[b,s,h] / 8 over 0 <= t - s <= window) v[b, s, h, :]; q/k/v/out bf16 with
- * strides (batch, token) in elements and heads of 64 channels side by side (head h at +64 h); T % 64 == 0.
+ * strides (batch, token) in elements and heads of 64 channels side by side (head h at +64 h); T % 128 == 0.
  * lse (optional, fp32 [batch, heads, T]) receives the log-sum-exp of each query's logits.
  * Replaces: utils/model.py:17-31 (attention / window_mask, flex_attention). */
 int noise_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t batch, int32_t heads, int64_t T,
@@ -145,10 +145,19 @@ int noise_adamw(float* p, const float* g, float* m, float* v, int64_t n, float l
 
 /* ---- a10, a11, a12: cross-token credit readout ------------------------------------------------------------ */
 
-/* lse[r, s] = log sum_{t in [s - window, s]} exp(q[r, s] . k[r, t] / 8); q, k bf16 [rows, T, 64], T % 64 == 0.
+/* lse[r, s] = log sum_{t in [s - window, s]} exp(q[r, s] . k[r, t] / 8); q, k bf16 [rows, T, 64], T % 128 == 0,
+ * rows <= 65535. The lse alone, for callers that need no center (train/val/run.py:965-985 builds A from it).
  * Replaces: train/speedrun/moment_kernels.py:79-110, 137-164 (_implicit_key_statistics, its lse output). */
 int noise_credit_lse(const uint16_t* q, const uint16_t* k, int64_t rows, int64_t T, int32_t window, float* lse,
                      void* stream);
+/* The key context of each receiver s: lse[r, s] as noise_credit_lse, and
+ * center[r, s] = sum_{t in [s - window, s]} exp(q[r, s] . k[r, t] / 8 - lse[r, s]) (hub[r, s] . values[r, t]),
+ * the softmax-weighted mean of the value scores. q, k, values, hub bf16 [rows, T, 64]; fp32 probabilities and
+ * accumulation; T % 128 == 0, rows <= 65535.
+ * Replaces: train/speedrun/moment_kernels.py:79-110 (_implicit_key_statistics), 137-164 (the _edges variant, same
+ * outputs up to summation order), 167-194 (_implicit_key_context / implicit_key_context_edges). */
+int noise_credit_key_context(const uint16_t* q, const uint16_t* k, const uint16_t* values, const uint16_t* hub,
+                             int64_t rows, int64_t T, int32_t window, float* lse, float* center, void* stream);
 
 /* out[r, t, :] = sum_{s in [t, t + window]} exp(k[r, t] . q[r, s] / 8 - lse[r, s]) src[r, s, :]; src fp32
  * [rows, T, 64] used as its bf16 high part (hi_lo != 0: high + low parts), probabilities in bf16, fp32 accumulation.

@@ -54,6 +54,7 @@ _SIGNATURES = {
     'noise_adamw': ([c_p, c_p, c_p, c_p, i64, f32, f32, f32, f32, f32, i64, c_p, c_p], ctypes.c_int),
     'noise_credit_lse': ([c_p, c_p, i64, i64, i32, c_p, c_p], ctypes.c_int),
     'noise_credit_value': ([c_p, c_p, c_p, c_p, i64, i64, i32, i32, c_p, c_p], ctypes.c_int),
+    'noise_credit_key_context': ([c_p, c_p, c_p, c_p, i64, i64, i32, c_p, c_p, c_p], ctypes.c_int),
 }
 
 EXPORTS = tuple(_SIGNATURES)
@@ -116,4 +117,4 @@ def timing_read():
     ms = (ctypes.c_double * n)()
     names = (ctypes.c_char_p * n)()
     k = lib().noise_timing_read(n, counts, ms, names)
-    return {names[c].decode(): (counts[c], ms[c]) for c in range(k)}
+    return {names[c].decode(): (counts[c], ms[c]) for c in range(min(k, n))}

@@ -7,8 +7,14 @@ train/speedrun/value_gluon.py:145-172): an LSE pass over each query's window, th
 out_t = sum_s exp(k_t . q_s / 8 - lse_s) src_s with bf16 probabilities, the source's bf16 high part (and optionally
 its low part) and fp32 accumulation.
 
-The ops are also registered as torch.library custom ops (noise_amd::credit_lse, noise_amd::raw_value_credits) with
-fake kernels, the operator API the reference's kernels use (moment_kernels.py:664-673).
+The key-context pass (moment_kernels.py:79-110, 137-194) returns lse and center_s = sum_t p(s, t) (hub_s . v_t) in
+one launch (key_context). value_pass takes exactly the arguments of moment_kernels._value_pass (:645-661), so it plugs
+into the reference's VALUE_IMPL hook (:642-643, set at train/speedrun/run.py:1678) and serves every value-credit op
+behind it, stacked and by-token layouts alike.
+
+The ops are also registered as torch.library custom ops (noise_amd::credit_lse, noise_amd::raw_value_credits,
+noise_amd::implicit_key_context_edges) with fake kernels, the operator API the reference's kernels use
+(moment_kernels.py:184-194, 664-673).
 """
 from __future__ import annotations
 
@@ -49,6 +55,61 @@ def raw_value_credits(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, hub: 
     return out
 
 
+def key_context(q: torch.Tensor, k: torch.Tensor, values: torch.Tensor, hub: torch.Tensor,
+                window: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(lse, center) [rows, T] fp32 of each receiver's window (moment_kernels._implicit_key_context): lse as
+    credit_lse, center_s = sum_t softmax_t(q_s . k_t / 8) (hub_s . values_t). Inputs (rows, T, 64), cast to bf16
+    (the speedrun feeds bf16 copies, train/speedrun/run.py:1770-1771); fp32 probabilities and sums."""
+    _lib.require_device(q, k, values, hub)
+    rows, T = _rows(q)
+    for name, t in (('k', k), ('values', values), ('hub', hub)):
+        if tuple(t.shape) != (rows, T, 64):
+            raise ValueError(f'{name} {tuple(t.shape)} does not match q {tuple(q.shape)}')
+    q, k, values, hub = (t.to(torch.bfloat16).contiguous() for t in (q, k, values, hub))
+    lse = torch.empty(rows, T, dtype=torch.float32, device=q.device)
+    center = torch.empty_like(lse)
+    _lib.call('noise_credit_key_context', _lib.ptr(q), _lib.ptr(k), _lib.ptr(values), _lib.ptr(hub), rows, T,
+              int(window), _lib.ptr(lse), _lib.ptr(center), _lib.stream(q.device))
+    return lse, center
+
+
+# HI: the value source's bf16 high part only, as value_gluon's CONFIG['HI'] (train/speedrun/value_gluon.py:20-21);
+# the default 0 adds the low part, as moment_kernels' Triton value kernel always does (moment_kernels.py:633-636).
+CONFIG = dict(HI=0)
+
+
+def value_pass(q, k, lse, source, window, in_heads=1, out_heads=1, out=None, layers=None, **over):
+    """moment_kernels._value_pass's arguments and result (train/speedrun/moment_kernels.py:645-661).
+
+    q, k (rows, T, 64); lse (rows, T); source stacked (rows, T, 64) or, with in_heads > 1, by token
+    (rows // in_heads, T, >= in_heads * 64) with row r = head r % in_heads of layer r // in_heads; the output stacked
+    or, with out_heads > 1, by token likewise, written into `out` (such a view, last stride 1) when given, layer l at
+    index layers[l] of its first axis when `layers` (int32) is given. Returns the output."""
+    h, t, d = q.shape
+    channels = source.shape[-1] // in_heads
+    if d != 64 or channels != 64:
+        raise ValueError(f'value_pass: head_dim {d} and source channels {channels} must be 64')
+    if source.stride(-1) != 1 or (out is not None and out.stride(-1) != 1):
+        raise AssertionError('value_pass: source and out need last stride 1')
+    cfg = dict(CONFIG, **over)
+    if in_heads == 1:
+        src = source
+    else:
+        src = source[..., :in_heads * 64].unflatten(-1, (in_heads, 64)).transpose(1, 2).reshape(h, t, 64)
+    res = raw_value_credits(q, k, lse, src, window, hi_lo=not cfg['HI'])
+    by_token = res.view(h // out_heads, out_heads, t, 64).transpose(1, 2).reshape(h // out_heads, t, out_heads * 64)
+    if out is None and layers is None:
+        return by_token
+    if out is None:
+        out = source.new_empty((h // out_heads, t, out_heads * 64), dtype=torch.float32)
+    dst = out[..., :out_heads * 64]
+    if layers is None:
+        dst.copy_(by_token)
+    else:
+        dst.index_copy_(0, layers.to(device=out.device, dtype=torch.long), by_token.to(out.dtype))
+    return out
+
+
 def value_credit(q: torch.Tensor, k: torch.Tensor, hub: torch.Tensor, window: int, hi_lo: bool = False) -> torch.Tensor:
     """Both passes: A^T @ hub for A = softmax(mask(q k^T / 8)) (Boost.value_credit), (rows, T, 64) in and out."""
     return raw_value_credits(q, k, credit_lse(q, k, window), hub, window, hi_lo)
@@ -73,3 +134,15 @@ def raw_value_credits_op(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, hu
 @raw_value_credits_op.register_fake
 def _(q, k, lse, hub, window):
     return torch.empty_like(hub, dtype=torch.float32)
+
+
+@torch.library.custom_op('noise_amd::implicit_key_context_edges', mutates_args=())
+def implicit_key_context_edges_op(q: torch.Tensor, k: torch.Tensor, values: torch.Tensor, hub: torch.Tensor,
+                                  window: int) -> tuple[torch.Tensor, torch.Tensor]:
+    return key_context(q, k, values, hub, window)
+
+
+@implicit_key_context_edges_op.register_fake
+def _(q, k, values, hub, window):
+    h, t, _ = q.shape
+    return q.new_empty((h, t), dtype=torch.float32), q.new_empty((h, t), dtype=torch.float32)

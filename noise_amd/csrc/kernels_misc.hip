@@ -116,6 +116,24 @@ extern "C" int noise_credit_lse(const uint16_t* q, const uint16_t* k, int64_t ro
   return NOISE_OK;
 }
 
+extern "C" int noise_credit_key_context(const uint16_t* q, const uint16_t* k, const uint16_t* values,
+                                        const uint16_t* hub, int64_t rows, int64_t T, int32_t window, float* lse,
+                                        float* center, void* stream) {
+  NOISE_REQUIRE(q && k && values && hub && lse && center, "NULL pointer argument");
+  NOISE_REQUIRE(rows > 0 && rows <= 65535, "rows outside [1, 65535]");
+  NOISE_REQUIRE(T > 0 && T % 128 == 0, "T = %lld must be a positive multiple of 128", (long long)T);
+  NOISE_REQUIRE(window >= 0, "negative window");
+  FlashArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = q; a.y = k; a.v = values; a.hub = hub;
+  a.x_sb = a.y_sb = a.v_sb = T * 64; a.x_st = a.y_st = a.v_st = 64;
+  a.lse_out = lse; a.center_out = center;
+  a.heads = 1; a.T = (int)T; a.window = window;
+  NoiseTimer tm(kTimeCreditCenter, (hipStream_t)stream);
+  NOISE_CHECK_HIP((launch_flash<kCenter, false, 1>(a, rows, 1, (hipStream_t)stream)));
+  return NOISE_OK;
+}
+
 extern "C" int noise_credit_value(const uint16_t* q, const uint16_t* k, const float* lse, const float* src, int64_t rows,
                                   int64_t T, int32_t window, int32_t hi_lo, float* out, void* stream) {
   NOISE_REQUIRE(q && k && lse && src && out, "NULL pointer argument");

@@ -6,6 +6,8 @@
 //           train/speedrun/moment_kernels.py:79-110
 //   kCredit out_o = sum_i exp(x_o . y_i / 8 - lse_i) v_i over 0 <= i - o <= W  (credit value pass; x = k, y = q,
 //           v = the fp32 source as bf16 high (+ low) parts)  train/speedrun/moment_kernels.py:612-661
+//   kCenter lse_o as kLse, and center_o = sum_i softmax_i(x_o . y_i / 8) (hub_o . v_i) over 0 <= o - i <= W
+//           (credit key-context pass; x = q, y = k, v = values)  train/speedrun/moment_kernels.py:79-110
 //
 // A workgroup owns 128 OG outputs of one (batch, head) row: 4 waves x OG groups of 32 outputs.
 // Inputs stream through two LDS stages in tiles of 64; the next tile's global loads are issued before the current
@@ -16,6 +18,9 @@
 // output groups of a wave. V^T is written to LDS in 8-byte chunks (4 inputs of one channel) after a 4x4 register
 // transpose; chunks are XOR-swizzled so a half-wave's reads hit distinct banks.
 //
+// kCenter computes the value scores the same way as the logits, S2^T[i, o] = v_i . hub_o (v staged in LDS like y,
+// hub in registers like x), and accumulates sum_i p_i s2_i beside sum_i p_i with fp32 probabilities.
+//
 // kAttn with BOUNDED (a.bound > 0): the model normalizes q and k (RMS over 64 channels, so |q| = |k| <= 8 and
 // |q . k / 8| <= 8); softmax weights are then exp(s - bound) in (e^-16, ~1] with no running maximum and no rescaling.
 #pragma once
@@ -24,12 +29,14 @@
 
 namespace noise {
 
-enum FlashMode { kAttn = 0, kLse = 1, kCredit = 2 };
+enum FlashMode { kAttn = 0, kLse = 1, kCredit = 2, kCenter = 3 };
 
 struct FlashArgs {
   const bf16_t* x;  // output-side vectors [batch, T, heads, 64] with strides below
   const bf16_t* y;  // input-side vectors
-  const void* v;    // values: bf16 (kAttn) or fp32 (kCredit)
+  const void* v;    // values: bf16 (kAttn, kCenter) or fp32 (kCredit)
+  const bf16_t* hub;  // kCenter: per-output vectors, same strides as x
+  float* center_out;  // kCenter: [batch * heads, T]
   int64_t x_sb, x_st, y_sb, y_st, v_sb, v_st;  // strides (elements) of batch and token; head h at +64 h
   const float* lse_in;  // kCredit: [batch * heads, T]
   void* out;            // kAttn: bf16 [batch, T, heads*64] (strides o_sb, o_st); kCredit: fp32 likewise
@@ -59,6 +66,12 @@ template <>
 struct FlashStage<kCredit> {
   u32x4 y[2];
   f32x4 v[4];  // kCredit: 4 inputs x 4 channels, fp32
+  float lse;
+};
+template <>
+struct FlashStage<kCenter> {
+  u32x4 y[2];
+  u32x4 v[2];  // kCenter: value rows, staged like y
   float lse;
 };
 
@@ -109,6 +122,18 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
       xf[og][kk] = *(const bf16x8*)(xg + (int64_t)o * a.x_st + kk * 16 + half * 8);
     }
 
+  bf16x8 hf[MODE == kCenter ? OG : 1][4];  // kCenter: hub fragments, laid out like xf
+  if constexpr (MODE == kCenter) {
+    const bf16_t* hg = a.hub + b * a.x_sb + head * 64;
+#pragma unroll
+    for (int og = 0; og < OG; ++og)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int o = wave_live ? ow + og * 32 + col : 0;
+        hf[og][kk] = *(const bf16x8*)(hg + (int64_t)o * a.x_st + kk * 16 + half * 8);
+      }
+  }
+
   f32x16 o_acc[OG][2];
 #pragma unroll
   for (int og = 0; og < OG; ++og)
@@ -116,9 +141,9 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o_acc[og][t][r] = 0.f;
-  float m_run[OG], l_run[OG];
+  float m_run[OG], l_run[OG], c_run[OG];
 #pragma unroll
-  for (int og = 0; og < OG; ++og) { m_run[og] = -INFINITY; l_run[og] = 0.f; }
+  for (int og = 0; og < OG; ++og) { m_run[og] = -INFINITY; l_run[og] = 0.f; c_run[og] = 0.f; }
   const float qk_scale = 0.125f * kLog2e;
   const float ref = bounded ? a.bound * kLog2e : 0.f;
 
@@ -133,7 +158,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
   i_begin = i_begin / kFlashBI * kFlashBI;
 
   const float* lse_in = (MODE == kCredit) ? a.lse_in + ((int64_t)b * a.heads + head) * T : nullptr;
-  const bf16_t* vgb = (MODE == kAttn) ? (const bf16_t*)a.v + b * a.v_sb + head * 64 : nullptr;
+  const bf16_t* vgb = (MODE == kAttn || MODE == kCenter) ? (const bf16_t*)a.v + b * a.v_sb + head * 64 : nullptr;
   const float* vgf = (MODE == kCredit) ? (const float*)a.v + b * a.v_sb + head * 64 : nullptr;
   const int kg = tid >> 4, dg = tid & 15;  // V staging: inputs 4 kg .. 4 kg + 3, channels 4 dg .. 4 dg + 3
 
@@ -153,6 +178,12 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
       for (int k = 0; k < 4; ++k)
         st.v[k] = *(const f32x4*)(vgf + (int64_t)(i0 + 4 * kg + k) * a.v_st + 4 * dg);
       st.lse = (tid < 64) ? lse_in[i0 + tid] : 0.f;
+    } else if constexpr (MODE == kCenter) {
+#pragma unroll
+      for (int rep = 0; rep < 2; ++rep) {
+        const int v = tid + rep * 256;
+        st.v[rep] = *(const u32x4*)(vgb + (int64_t)(i0 + (v >> 3)) * a.v_st + (v & 7) * 8);
+      }
     }
   };
   auto store = [&](int s, const FlashStage<MODE>& st) {
@@ -189,6 +220,13 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
         *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
       }
       if (tid < 64) lse_s[s][tid] = st.lse;
+    } else if constexpr (MODE == kCenter) {
+#pragma unroll
+      for (int rep = 0; rep < 2; ++rep) {
+        const int v = tid + rep * 256;
+        const int row = v >> 3, chunk = v & 7;
+        *(u32x4*)(&vt_hi[s][row * 64 + ((chunk ^ ((row >> 1) & 7)) * 8)]) = st.v[rep];
+      }
     }
   };
 
@@ -222,21 +260,37 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
     if (any_og) {
       // ---- S^T = Y X^T for both output groups; each y fragment is read once ----
       f32x16 sc[OG][2];
+      f32x16 s2[MODE == kCenter ? OG : 1][2];  // kCenter: value scores v_i . hub_o
 #pragma unroll
       for (int og = 0; og < OG; ++og)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) sc[og][t][r] = 0.f;
+      if constexpr (MODE == kCenter) {
+#pragma unroll
+        for (int og = 0; og < OG; ++og)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s2[og][t][r] = 0.f;
+      }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int row = t * 32 + col;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8 yf = *(const bf16x8*)(&ys[s][row * 64 + (((kk * 2 + half) ^ ((row >> 1) & 7)) * 8)]);
+          const int at = row * 64 + (((kk * 2 + half) ^ ((row >> 1) & 7)) * 8);
+          const bf16x8 yf = *(const bf16x8*)(&ys[s][at]);
 #pragma unroll
           for (int og = 0; og < OG; ++og)
             if (any[og]) sc[og][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yf, xf[og][kk], sc[og][t], 0, 0, 0);
+          if constexpr (MODE == kCenter) {
+            const bf16x8 vf = *(const bf16x8*)(&vt_hi[s][at]);
+#pragma unroll
+            for (int og = 0; og < OG; ++og)
+              if (any[og]) s2[og][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, hf[og][kk], s2[og][t], 0, 0, 0);
+          }
         }
       }
 
@@ -285,7 +339,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
           const float m_new = fmaxf(m_run[og], mt);
           const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
           const float corr = fast_exp2(m_run[og] - m_safe);
-          float ls = 0.f;
+          float ls = 0.f, cs = 0.f;
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -293,8 +347,10 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
               const float p = fast_exp2(sc[og][t][r] - m_safe);
               sc[og][t][r] = p;
               ls += p;
+              if constexpr (MODE == kCenter) cs = fmaf(p, s2[og][t][r], cs);
             }
           l_run[og] = l_run[og] * corr + ls;
+          if constexpr (MODE == kCenter) c_run[og] = c_run[og] * corr + cs;
           m_run[og] = m_new;
           if (MODE == kAttn) {
 #pragma unroll
@@ -306,7 +362,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
       }
 
       // ---- O^T += V^T P^T: 4 k-steps of 16 inputs, 2 tiles of 32 channels; V^T fragments shared by both groups ----
-      if (MODE != kLse) {
+      if (MODE == kAttn || MODE == kCredit) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -349,11 +405,15 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
 #pragma unroll
   for (int og = 0; og < OG; ++og) {
     const int my_o = ow + og * 32 + col;
-    if (MODE == kAttn || MODE == kLse) {
+    if (MODE == kAttn || MODE == kLse || MODE == kCenter) {
       const float l_tot = l_run[og] + __shfl_xor(l_run[og], 32, 64);
       const float mref = bounded ? ref : m_run[og];
       const float lse = (mref + log2f(l_tot)) * (1.0f / kLog2e);
       if (a.lse_out && half == 0) a.lse_out[((int64_t)b * a.heads + head) * T + my_o] = lse;
+      if constexpr (MODE == kCenter) {
+        const float c_tot = c_run[og] + __shfl_xor(c_run[og], 32, 64);
+        if (half == 0) a.center_out[((int64_t)b * a.heads + head) * T + my_o] = c_tot / l_tot;
+      }
       if (MODE == kAttn) {
         const float inv = 1.0f / l_tot;
         bf16_t* og_ptr = (bf16_t*)a.out + b * a.o_sb + (int64_t)my_o * a.o_st + head * 64;

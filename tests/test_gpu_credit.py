@@ -1,7 +1,9 @@
 """GPU parity of the credit readout (rows a10-a12) and the attention forward (a5) against the oracle.
 
 Tolerances: credit outputs within 2e-2 max relative error (max |gpu - ref| / max |ref|, the bound BASELINE.json
-states), lse within 2e-2 absolute (bf16 operands; logits up to 8 in magnitude)."""
+states), lse within 2e-2 absolute (bf16 operands; logits up to 8 in magnitude). The key context takes bf16 inputs that
+the oracle then uses exactly (bf16 products are exact in the fp32 MFMA accumulation, as in the reference's tf32 dots of
+bf16 moments), so it is held to 1e-4: lse absolute, center relative to max |center|."""
 import numpy as np
 import pytest
 import torch
@@ -83,3 +85,79 @@ def test_attention_forward(dev, T, window):
     ref = om.attention(q.bfloat16().float(), k.bfloat16().float(), v.bfloat16().float(), window)
     out = attention(q.to(dev), k.to(dev), v.to(dev), window).float().cpu()
     assert _relmax(out, ref) < 2e-2
+
+
+def _bf(rows, T, seed, scale=1.0):
+    return (torch.randn(rows, T, 64, generator=torch.Generator().manual_seed(seed)) * scale).bfloat16()
+
+
+@pytest.mark.parametrize('T,window,unit', [(256, 256, True), (256, 64, False), (384, 128, True), (128, 0, True),
+                                           (2048, 1024, True)])
+def test_key_context(dev, T, window, unit):
+    from noise_amd import credit
+    print(f'key_context T={T} window={window} unit={unit}', flush=True)
+    rows = 2 if T > 1024 else 3
+    q, k = _qk(rows, T, unit, seed=T + 3 * window)
+    values, hub = _bf(rows, T, 11), _bf(rows, T, 12)
+    lse_ref, c_ref = oc.key_context(q.double(), k.double(), values.double(), hub.double(), window)
+    lse, c = credit.key_context(q.to(dev), k.to(dev), values.to(dev), hub.to(dev), window)
+    assert (lse.cpu().double() - lse_ref).abs().max().item() < 1e-4
+    assert _relmax(c.cpu().double(), c_ref) < 1e-4
+    op_lse, op_c = torch.ops.noise_amd.implicit_key_context_edges(q.to(dev), k.to(dev), values.to(dev),
+                                                                  hub.to(dev), window)
+    assert torch.equal(op_lse, lse) and torch.equal(op_c, c)
+
+
+def test_key_context_q0_closed_form(dev):
+    from noise_amd import credit
+    T, W = 256, 77
+    q = torch.zeros(2, T, 64, dtype=torch.bfloat16)
+    k, values, hub = _bf(2, T, 1), _bf(2, T, 2), _bf(2, T, 3)
+    _, c = credit.key_context(q.to(dev), k.to(dev), values.to(dev), hub.to(dev), W)
+    ref = oc.key_context_q0_closed_form(values.double(), hub.double(), W)
+    assert _relmax(c.cpu().double(), ref) < 1e-4
+
+
+def test_key_context_constant_values_c3_shape(dev):
+    """Config 3 at full size (B16 H8 T2048): constant values make center_s = hub_s . v for any logits."""
+    from noise_amd import credit
+    print('key_context constant values B16 H8 T2048', flush=True)
+    rows, T = 16 * 8, 2048
+    g = torch.Generator(device=dev).manual_seed(4)
+    q, k = (om.rms_norm(torch.randn(rows, T, 64, device=dev, generator=g)).bfloat16() for _ in range(2))
+    hub = torch.randn(rows, T, 64, device=dev, generator=g).bfloat16()
+    v = torch.randn(64, device=dev, generator=g).bfloat16()
+    values = v.expand(rows, T, 64).contiguous()
+    want = hub.double() @ v.double()
+    for window in (T, 1024):
+        _, c = credit.key_context(q, k, values, hub, window)
+        assert _relmax(c.double(), want) < 1e-4, window
+
+
+def test_value_pass_layouts(dev):
+    """moment_kernels._value_pass layouts through the VALUE_IMPL adapter: stacked, by-token in, by-token out, and a
+    caller-owned by-token view with mapped layers; all are permutations of the stacked result, bit for bit."""
+    from noise_amd import credit
+    H, L, T, W = 3, 2, 256, 100
+    rows = H * L
+    q, k = _qk(rows, T, True, seed=21)
+    q, k = q.to(dev), k.to(dev)
+    src = torch.randn(rows, T, 64, generator=torch.Generator().manual_seed(22)).to(dev)
+    lse = credit.credit_lse(q, k, W)
+    base = credit.value_pass(q, k, lse, src, W)
+    ref = oc.value_pass(q.float().cpu(), k.float().cpu(), lse.cpu(), src.cpu(), W)
+    assert _relmax(base.cpu(), ref) < 1e-2
+    src_bt = oc.by_token(src.cpu(), H).to(dev)
+    assert torch.equal(credit.value_pass(q, k, lse, src_bt, W, in_heads=H), base)
+    out_bt = credit.value_pass(q, k, lse, src, W, out_heads=H)
+    assert torch.equal(out_bt.cpu(), oc.by_token(base.cpu(), H))
+    buf = torch.zeros(4, T, 2 * H * 64, device=dev)
+    view = buf[:, :, H * 64:]
+    layers = torch.tensor([3, 1], dtype=torch.int32, device=dev)
+    got = credit.value_pass(q, k, lse, src_bt, W, in_heads=H, out_heads=H, out=view, layers=layers)
+    assert got.data_ptr() == view.data_ptr()
+    want = oc.by_token(base.cpu(), H)
+    assert torch.equal(buf[3, :, H * 64:].cpu(), want[0]) and torch.equal(buf[1, :, H * 64:].cpu(), want[1])
+    assert not buf[0].any() and not buf[2].any() and not buf[:, :, :H * 64].any()
+    hi = credit.value_pass(q, k, lse, src, W, HI=1)
+    assert _relmax(hi.cpu(), ref) < 2e-2 and not torch.equal(hi, base)

@@ -61,3 +61,60 @@ def test_planted_transpose_fails_conservation():
     q, k, e = _inputs()
     wrong = oc.attention_maps(q, k, 9) @ e
     assert not torch.allclose(wrong.sum(-2), e.sum(-2), atol=1e-6)
+
+
+@pytest.mark.parametrize('window', [0, 5, 39])
+def test_key_context_constant_values(window):
+    """Every softmax row sums to 1, so constant values give center_s = hub_s . v exactly."""
+    q, k, hub = _inputs()
+    v = torch.randn(64, dtype=torch.float64)
+    values = v.expand(2, 40, 64).clone()
+    lse_, center = oc.key_context(q, k, values, hub, window)
+    assert torch.allclose(center, hub @ v, atol=1e-10)
+    assert torch.allclose(lse_, oc.lse(q, k, window), atol=1e-12)
+
+
+def test_key_context_q0_closed_form():
+    _, k, hub = _inputs()
+    values = _inputs(seed=5)[2]
+    q = torch.zeros(2, 40, 64, dtype=torch.float64)
+    for window in (0, 7, 39):
+        got = oc.key_context(q, k, values, hub, window)[1]
+        assert torch.allclose(got, oc.key_context_q0_closed_form(values, hub, window), atol=1e-10)
+
+
+def test_key_context_bruteforce():
+    q, k, hub = _inputs(T=11, rows=1)
+    values = _inputs(T=11, rows=1, seed=9)[0]
+    W = 3
+    lse_, center = oc.key_context(q, k, values, hub, W)
+    for s in range(11):
+        ts = range(max(0, s - W), s + 1)
+        logits = torch.stack([q[0, s] @ k[0, t] / 8 for t in ts])
+        p = torch.softmax(logits, 0)
+        want = sum(p[j] * (hub[0, s] @ values[0, t]) for j, t in enumerate(ts))
+        assert abs(center[0, s].item() - want.item()) < 1e-12
+        assert abs(lse_[0, s].item() - torch.logsumexp(logits, 0).item()) < 1e-12
+
+
+def test_planted_transposed_probabilities_fail():
+    """center from p[t, s] instead of p[s, t] (a transposed softmax) breaks the constant-values identity."""
+    q, k, hub = _inputs()
+    v = torch.randn(64, dtype=torch.float64)
+    values = v.expand(2, 40, 64).clone()
+    lse_ = oc.lse(q, k, 9)
+    logits = ((q @ k.transpose(-1, -2)) / 8).masked_fill(~oc._mask(40, 9), float('-inf'))
+    p = torch.exp(logits - lse_.unsqueeze(-1))
+    wrong = (p.transpose(-1, -2) * (hub @ values.transpose(-1, -2))).sum(-1)
+    assert not torch.allclose(wrong, hub @ v, atol=1e-6)
+    assert torch.allclose(oc.key_context(q, k, values, hub, 9)[1], hub @ v, atol=1e-10)
+
+
+def test_by_token_layout():
+    """Row r of the stacked layout is head r % H of layer r // H (moment_kernels.py:67-74), by explicit indexing."""
+    x = torch.arange(6 * 5 * 4, dtype=torch.float64).reshape(6, 5, 4)
+    H = 3
+    bt = oc.by_token(x, H)
+    for r in range(6):
+        assert torch.equal(bt[r // H, :, (r % H) * 4:(r % H + 1) * 4], x[r])
+    assert torch.equal(oc.stacked(bt, H), x)
