@@ -58,7 +58,7 @@ int noise_rng_rows(uint64_t seed, const int64_t* offsets, int64_t pairs, const i
 /* y[i, t, :] = x[i, t, :] W^T + sign[i] (x[i, t, :] . b_i) a_i, a_i = noise[i * noise_stride + a_off + (0..out)],
  * b_i = noise[i * noise_stride + b_off + (0..in)]; x bf16 [m, T, in] (x_shared != 0: one [T, in] for every member),
  * W bf16 [out, in]. Outputs (either may be NULL): y fp32 [m, T, out]; sumsq fp32 [m] = sum of y^2 per member.
- * T % 128 == 0, in % 64 == 0, out % 256 == 0.
+ * T % 128 == 0, in % 32 == 0, out % 256 == 0.
  * Replaces: archive/10M/train/val/eggroll.py:56-58 (lowrank). */
 int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t* w, const float* noise, int64_t noise_stride,
                   int64_t a_off, int64_t b_off, const float* sign, int64_t m, int64_t T, int64_t in, int64_t out,

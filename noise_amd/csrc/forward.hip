@@ -429,7 +429,7 @@ __global__ __launch_bounds__(256) void member_sum_kernel(const float* __restrict
   if (threadIdx.x == 0) out[m] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-using Tile = GemmShape<256, 256, 64, 2, 2>;
+using Tile = GemmShape<256, 256, 32, 2, 2>;
 constexpr int kAttnOG = 1;  // 32 outputs per wave (2 waves per SIMD)
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }

@@ -2,11 +2,14 @@
 // the x @ weight.t() of nn.Linear weights stored [out, in]). The accumulator tile goes to an epilogue functor, which
 // is where the population-specific work (rank-1 member corrections, residual adds, relu^2, soft-capped CE) happens.
 //
-// Tiling: a workgroup computes BM x BN with WM x WN waves; a wave owns (BM/WM) x (BN/WN) as 32x32 MFMA tiles
-// (v_mfma_f32_32x32x16_bf16). K advances in BK steps through two LDS buffers: the next step's buffer loads are issued
-// before the current step's MFMAs and stored to the other buffer after them (one barrier per step).
-// LDS rows are BK bf16 = BK/8 16-byte chunks, XOR-swizzled (swz below) so that every ds_read_b128 / ds_write_b128
-// phase is free of bank conflicts.
+// Tiling: a workgroup computes 256 x 256 with 2 x 2 waves; a wave owns 128 x 128 as 4 x 4 MFMA tiles
+// (v_mfma_f32_32x32x16_bf16). K advances in steps of 32 through kStages LDS stages filled by direct-to-LDS buffer
+// loads (buffer_load_dwordx4 ... lds): the loads of step kt + kStages are issued as soon as every wave is done with
+// step kt, so up to three steps of loads are in flight behind the MFMAs and no register holds staged data.
+// One barrier per step, placed between the step's two 16-deep k-substeps: the second k-substep's fragments are
+// read before it and the next step's first fragments after it, so LDS latency hides behind MFMAs.
+// An LDS row is 32 bf16 = 4 16-byte chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 lanes of a
+// ds_read_b128 phase (16 consecutive rows, one chunk) touch 16 distinct bank groups.
 //
 // MFMA 32x32x16 bf16 lane layout (checked on gfx950): lane l supplies A[row l%32][k 8(l/32)..8(l/32)+7] and
 // B^T[col l%32][same k]; accumulator register r holds C[row (r/4)*8 + (l/32)*4 + r%4][col l%32].
@@ -26,35 +29,44 @@ struct GemmShape {
   static constexpr int kThreads = WM * WN * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
-  static constexpr int kChunks = BK / 8;              // 16-byte chunks per LDS row
-  static constexpr int kAVec = BM * kChunks / kThreads;  // 16-byte global loads per thread
-  static constexpr int kBVec = BN * kChunks / kThreads;
-  static constexpr int kEpiLd = BN + 16;                // bf16 staging row stride (16 elements of padding)
-  static constexpr int kMainLds = 2 * (BM + BN) * BK * 2;
+  static constexpr int kStages = 4;
+  static constexpr int kStageBytes = (BM + BN) * BK * 2;  // A rows then B rows
+  static constexpr int kEpiLd = BN + 16;                  // bf16 staging row stride (16 elements of padding)
+  static constexpr int kMainLds = kStages * kStageBytes;
   static constexpr int kEpiLds = BM * kEpiLd * 2;         // the whole tile in bf16
   static constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
-  static_assert(BK % 16 == 0 && kChunks <= 8 && kChunks >= 2, "BK in {16, 32, 64}");
-  static_assert((BM * kChunks) % kThreads == 0 && (BN * kChunks) % kThreads == 0, "tile loads must divide threads");
+  static_assert(BM == 256 && BN == 256 && BK == 32 && WM == 2 && WN == 2, "the main loop is written for 256x256x32");
 };
 
-// 16-byte chunk c of LDS row r is stored at c ^ ((r >> 1) & (kChunks - 1)): a ds_read_b128 / ds_write_b128 phase
-// (16 lanes, 256 bytes) then touches 16 distinct bank groups both for fragment reads (16 consecutive rows, one chunk)
-// and for tile stores (2 rows x 8 chunks).
-template <int kChunks>
-__device__ __forceinline__ int swz(int row, int chunk) {
-  return chunk ^ ((row >> 1) & (kChunks - 1));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt vmcnt(n) for n in {0, 8, 16, 24}, expcnt and lgkmcnt left alone (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  if (n >= 24) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8) | (1 << 14));
+  else if (n >= 16) __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8) | (1 << 14));
+  else if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));
+  else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+}
+constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0)
+
+// Workgroup barrier without a memory fence: the fence of __syncthreads would also wait for every load still in
+// flight into LDS. The empty asm statements keep the compiler from moving memory accesses across it; the waits
+// before it are explicit.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 template <class S, class Epi>
 __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __restrict__ A, int64_t lda,
                                                               const bf16_t* __restrict__ B, int64_t ldb, int M, int N,
                                                               int K, Epi epi) {
-  static_assert(S::BK == 64, "main loop: 8 chunks of 16 bytes per LDS row");
+  constexpr int NS = S::kStages;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  // LDS (bytes): A stage s at s * kAStage, B stage s at 2 * kAStage + s * kBStage. Every LDS access below is a
-  // per-lane base register plus an immediate offset (< 64 KB).
-  constexpr int kAStage = S::BM * S::BK * 2, kBStage = S::BN * S::BK * 2;
+  constexpr int kAStage = S::BM * S::BK * 2;  // 16 KB of A rows, then 16 KB of B rows
+  constexpr int kStage = S::kStageBytes;
 
   // Workgroups are dispatched round-robin over the 8 XCDs; tiles are renumbered so that each XCD walks a contiguous
   // run of tiles (its A panels and B tiles are then fetched into one XCD's L2). Within a run, tiles go in groups of
@@ -72,27 +84,47 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   const int wm = wave / S::WN, wn = wave % S::WN;
   const int a_rows = min(S::BM, M - m0), b_rows = min(S::BN, N - n0);
 
-  // Buffer resources over this tile's rows: reads past the last row return zeros. The K step and the row pass go
-  // in the scalar offset, so a load costs no vector address arithmetic.
+  // Buffer resources over this tile's rows. The row goes in the per-lane offset, which the range check covers, so
+  // rows past the last one read as zeros; the K step goes in the scalar offset.
   const __amdgpu_buffer_rsrc_t a_rsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)(A + (int64_t)m0 * lda), 0, a_rows * (int)lda * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t b_rsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)(B + (int64_t)n0 * ldb), 0, b_rows * (int)ldb * 2, 0x00020000);
-  constexpr int kRowsPerPass = S::kThreads / S::kChunks;  // rows covered by one 16-byte load per thread
-  const int lrow = threadIdx.x / S::kChunks, lchunk = threadIdx.x % S::kChunks;
-  const int a_voff = (lrow * (int)lda + lchunk * 8) * 2, b_voff = (lrow * (int)ldb + lchunk * 8) * 2;
-  const int a_pass = kRowsPerPass * (int)lda * 2, b_pass = kRowsPerPass * (int)ldb * 2;
-  const int st_off = (lrow * S::BK + swz<S::kChunks>(lrow, lchunk) * 8) * 2;  // rows lrow + 32 i share the swizzle
 
-  // fragment offsets for each 16-deep k-substep (row bits 1..3 = lane bits 1..3)
-  const int xs = ((lane & 31) >> 1) & 7;
-  int fa_off[S::BK / 16], fb_off[S::BK / 16];
+  // One direct-to-LDS load fills 1 KB = 16 rows x 4 chunks: lane l writes LDS bytes 16 l .. 16 l + 15, i.e. row
+  // l >> 2, slot l & 3, so it fetches global chunk (l & 3) ^ ((l >> 4) & 3). Wave w fills row groups 4 w .. 4 w + 3
+  // of A and of B.
+  const int drow = lane >> 2, dchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  int a_vo[4], b_vo[4];
 #pragma unroll
-  for (int kk = 0; kk < S::BK / 16; ++kk) {
+  for (int j = 0; j < 4; ++j) {
+    const int r = (wave * 4 + j) * 16 + drow;
+    a_vo[j] = (r * (int)lda + dchunk * 8) * 2;
+    b_vo[j] = (r * (int)ldb + dchunk * 8) * 2;
+  }
+  auto dma = [&](int kt, int stage) {
+    const int koff = kt * S::BK * 2;
+    unsigned char* base = smem_raw + stage * kStage + wave * 4 * 1024;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(base + j * 1024), 16, a_vo[j], koff, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kAStage + j * 1024), 16, b_vo[j], koff, 0,
+                                               0);
+  };
+
+  // Fragment offsets: row (lane & 31) of a 32-row tile, chunk 2 kk + (lane >> 5), in slot chunk ^ row bits 2..3.
+  const int xs = ((lane & 31) >> 2) & 3;
+  int fa_off[2], fb_off[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
     const int ch = ((2 * kk + (lane >> 5)) ^ xs) * 16;
     fa_off[kk] = (wm * S::WTM + (lane & 31)) * S::BK * 2 + ch;
-    fb_off[kk] = 2 * kAStage + (wn * S::WTN + (lane & 31)) * S::BK * 2 + ch;
+    fb_off[kk] = kAStage + (wn * S::WTN + (lane & 31)) * S::BK * 2 + ch;
   }
+  auto frag = [&](int off) { return *(const bf16x8*)(smem_raw + off); };
+  constexpr int kTileStride = 32 * S::BK * 2;  // bytes between the 32-row MFMA tiles of a stage
 
   f32x16 acc[S::TM][S::TN];
 #pragma unroll
@@ -102,59 +134,53 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  u32x4 ra[S::kAVec], rb[S::kBVec];
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < S::kAVec; ++i)
-      ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, i * a_pass + kt * S::BK * 2, 0));
-#pragma unroll
-    for (int i = 0; i < S::kBVec; ++i)
-      rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, b_voff, i * b_pass + kt * S::BK * 2, 0));
-  };
-  auto lstore = [&](int stage) {
-    const int sa = stage * kAStage, sb = 2 * kAStage + stage * kBStage;
-#pragma unroll
-    for (int i = 0; i < S::kAVec; ++i) *(u32x4*)(smem_raw + sa + st_off + i * kRowsPerPass * S::BK * 2) = ra[i];
-#pragma unroll
-    for (int i = 0; i < S::kBVec; ++i) *(u32x4*)(smem_raw + sb + st_off + i * kRowsPerPass * S::BK * 2) = rb[i];
-  };
-  auto frag = [&](int off) { return *(const bf16x8*)(smem_raw + off); };
-
   const int nk = K / S::BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
+  // Prologue: steps 0 .. NS - 1 in flight; stage 0 visible; its first k-substep's fragments read.
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (s < nk) dma(s, s);
+  wait_vmcnt(8 * min(nk - 1, NS - 1));
+  lds_barrier();
+  bf16x8 f0a[S::TM], f0b[S::TN], f1a[S::TM], f1b[S::TN];
+#pragma unroll
+  for (int i = 0; i < S::TM; ++i) f0a[i] = frag(fa_off[0] + i * kTileStride);
+#pragma unroll
+  for (int j = 0; j < S::TN; ++j) f0b[j] = frag(fb_off[0] + j * kTileStride);
 
-  // K steps on LDS stage P = kt & 1: issue the next step's loads, run the MFMAs (fragments of k-substep kk + 1 are
-  // read while those of kk multiply), store the loaded step to stage P ^ 1, barrier
+  // Step kt on stage kt % NS: read k-substep 1 and multiply k-substep 0; wait for this wave's reads and for stage
+  // kt + 1's loads, barrier (everyone is then past its reads of stage kt, and stage kt + 1 is visible); refill stage
+  // kt % NS with step kt + NS; read the next step's k-substep 0 and multiply k-substep 1.
   for (int kt = 0; kt < nk; ++kt) {
-    const int P = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) gload(kt + 1);
-    const int pa = P * kAStage, pb = P * kBStage;
-    bf16x8 fa[2][S::TM], fb[2][S::TN];
+    const int pb = (kt % NS) * kStage;
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i) fa[0][i] = frag(fa_off[0] + pa + i * 32 * S::BK * 2);
+    for (int i = 0; i < S::TM; ++i) f1a[i] = frag(fa_off[1] + pb + i * kTileStride);
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) fb[0][j] = frag(fb_off[0] + pb + j * 32 * S::BK * 2);
+    for (int j = 0; j < S::TN; ++j) f1b[j] = frag(fb_off[1] + pb + j * kTileStride);
 #pragma unroll
-    for (int kk = 0; kk < S::BK / 16; ++kk) {
-      const int c = kk & 1;
-      if (kk + 1 < S::BK / 16) {
+    for (int i = 0; i < S::TM; ++i)
 #pragma unroll
-        for (int i = 0; i < S::TM; ++i) fa[c ^ 1][i] = frag(fa_off[kk + 1] + pa + i * 32 * S::BK * 2);
+      for (int j = 0; j < S::TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0a[i], f0b[j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    wait_vmcnt(8 * max(0, min(nk - 2 - kt, NS - 2)));
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + NS < nk) dma(kt + NS, kt % NS);
+    if (kt + 1 < nk) {
+      const int nb = ((kt + 1) % NS) * kStage;
 #pragma unroll
-        for (int j = 0; j < S::TN; ++j) fb[c ^ 1][j] = frag(fb_off[kk + 1] + pb + j * 32 * S::BK * 2);
-      }
+      for (int i = 0; i < S::TM; ++i) f0a[i] = frag(fa_off[0] + nb + i * kTileStride);
 #pragma unroll
-      for (int i = 0; i < S::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < S::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][i], fb[c][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < S::TN; ++j) f0b[j] = frag(fb_off[0] + nb + j * kTileStride);
     }
-    if (more) lstore(P ^ 1);
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < S::TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1a[i], f1b[j], acc[i][j], 0, 0, 0);
   }
+  __syncthreads();  // every wave is done reading the stages before the epilogue reuses the LDS
 
   // Epilogue through LDS. The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul
   // output, to which it then adds its fp32 rank-1 term -- and staged as the whole 256 x 256 tile. Each wave then takes

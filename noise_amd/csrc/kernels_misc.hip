@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void member_part_sum_kernel(const float* __res
   if (threadIdx.x == 0) out[m] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-using LTile = GemmShape<256, 256, 64, 2, 2>;
+using LTile = GemmShape<256, 256, 32, 2, 2>;
 
 }  // namespace noise
 
@@ -168,7 +168,7 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
   NOISE_REQUIRE(x && w && noise && sign, "NULL pointer argument");
   NOISE_REQUIRE(m > 0 && T > 0 && T % LTile::WTM == 0, "T = %lld must be a positive multiple of %d", (long long)T,
                 LTile::WTM);
-  NOISE_REQUIRE(in > 0 && in % LTile::BK == 0 && out > 0 && out % LTile::BN == 0, "in %% 64 and out %% 256 must be 0");
+  NOISE_REQUIRE(in > 0 && in % LTile::BK == 0 && out > 0 && out % LTile::BN == 0, "in %% 32 and out %% 256 must be 0");
   const int64_t M = m * T;
   NOISE_REQUIRE(M <= (int64_t)INT32_MAX / 4, "m * T too large");
   NOISE_REQUIRE(workspace && workspace_bytes >= noise_lowrank_workspace(m, T, in, out, x_shared),
