@@ -38,6 +38,12 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
+// x as held by lane idx; idx must be the same in every lane (v_readlane_b32).
+__device__ __forceinline__ float lane_val(float x, int idx) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), idx));
+}
+__device__ __forceinline__ int lane_val(int x, int idx) { return __builtin_amdgcn_readlane(x, idx); }
+
 // Sums of 8 per-lane values over the 64 lanes, by a transposed butterfly (10 shuffles instead of 8 x 6): returns
 // the total of value (4 b5 + 2 b4 + b3) where b5 b4 b3 are bits 5..3 of the lane id (8 lanes hold each total).
 __device__ __forceinline__ float warp_sum8(const float (&p)[8], int lane) {

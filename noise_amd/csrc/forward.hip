@@ -189,37 +189,78 @@ struct EpiQKV {
   int Vp;
   const float* cos_t;  // [T, 32]
   const float* sin_t;
-  template <int R>
-  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, f32x4 (&v)[R]) const {
-    const int m = mb.member(row0);
-    const float* nr = mb.nrow(m);
-    const float s = mb.sgn(m);
-    const int seg = n0 >> 9;
-    const int c = (n0 & (kD - 1)) + 4 * lane;
-    const int t0 = row0 - m * mb.T;
-    if (nr) {
-      const f32x4 a = ld4(nr + off[seg] + c);
-      float k[R];
-#pragma unroll
-      for (int q = 0; q < R; ++q) k[q] = xb[(int64_t)(row0 + q) * 4 + seg];
-#pragma unroll
-      for (int q = 0; q < R; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[q][e] += s * k[q] * a[e];
+  struct Wave {
+    int row_base, t0, seg, c;
+    const float* nr;
+    float s, xb, at;
+    int tok;
+    f32x4 a, b_ve;
+  };
+  struct Pre {
+    f32x4 p0[kEpiRows], p1[kEpiRows];  // q / k columns: cos, sin rows; v columns: value-embedding rows (p0)
+    float g[kEpiRows];                 // v columns: gates
+  };
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+    const int m = mb.member(row_base);
+    w.row_base = row_base;
+    w.t0 = row_base - m * mb.T;
+    w.seg = n0 >> 9;
+    w.c = (n0 & (kD - 1)) + 4 * lane;
+    w.nr = mb.nrow(m);
+    w.s = mb.sgn(m);
+    w.xb = 0.f; w.at = 0.f; w.tok = 0;
+    w.a = w.b_ve = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (w.nr) {
+      w.a = ld4(w.nr + off[w.seg] + w.c);
+      w.xb = xb[(int64_t)(row_base + lane) * 4 + w.seg];
     }
-    if (seg < 2) {
+    if (w.seg == 2 && ve) {
+      const int64_t tk = mb.tokens[(int64_t)mb.seq[m] * mb.T + w.t0 + lane];
+      w.tok = (tk < 0 || tk >= Vp) ? 0 : (int)tk;
+      if (w.nr) {
+        w.at = w.s * w.nr[off_ve + w.tok];
+        w.b_ve = ld4(w.nr + off_ve + Vp + w.c);
+      }
+    }
+  }
+  __device__ __forceinline__ void load(int row0, int, int lane, const Wave& w, Pre& p) const {
+    const int i0 = row0 - w.row_base;
+    if (w.seg < 2) {
       const int j = 4 * (lane & 7);
-      const bool first = (lane & 15) < 8;
-      f32x4 cs[R], sn[R];
 #pragma unroll
-      for (int q = 0; q < R; ++q) { cs[q] = ld4(cos_t + (t0 + q) * 32 + j); sn[q] = ld4(sin_t + (t0 + q) * 32 + j); }
+      for (int q = 0; q < kEpiRows; ++q) {
+        p.p0[q] = ld4(cos_t + (w.t0 + i0 + q) * 32 + j);
+        p.p1[q] = ld4(sin_t + (w.t0 + i0 + q) * 32 + j);
+      }
+    } else if (ve) {
+#pragma unroll
+      for (int q = 0; q < kEpiRows; ++q) {
+        p.p0[q] = ld4(ve + (int64_t)lane_val(w.tok, i0 + q) * kD + w.c);
+        p.g[q] = gate[(int64_t)(row0 + q) * kH + (w.c >> 6)];
+      }
+    }
+  }
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, const Wave& w, const Pre& p,
+                                       f32x4 (&v)[R]) const {
+    const int i0 = row0 - w.row_base;
+    if (w.nr) {
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const float k = lane_val(w.xb, i0 + q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[q][e] += w.s * k * w.a[e];
+      }
+    }
+    if (w.seg < 2) {
+      const bool first = (lane & 15) < 8;
 #pragma unroll
       for (int q = 0; q < R; ++q) {
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float other = __shfl_xor(v[q][e], 8, 64);
-          v[q][e] = first ? v[q][e] * cs[q][e] + other * sn[q][e] : -other * sn[q][e] + v[q][e] * cs[q][e];
+          v[q][e] = first ? v[q][e] * p.p0[q][e] + other * p.p1[q][e] : -other * p.p1[q][e] + v[q][e] * p.p0[q][e];
           ss += v[q][e] * v[q][e];
         }
 #pragma unroll
@@ -229,25 +270,12 @@ struct EpiQKV {
         for (int e = 0; e < 4; ++e) v[q][e] *= inv;
       }
     } else if (ve) {
-      int64_t tok[R];
-      float g[R], at[R];
-      f32x4 e4[R];
 #pragma unroll
       for (int q = 0; q < R; ++q) {
-        const int64_t tk = mb.tokens[(int64_t)mb.seq[m] * mb.T + t0 + q];
-        tok[q] = (tk < 0 || tk >= Vp) ? 0 : tk;
+        const float at = lane_val(w.at, i0 + q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[q][e] += p.g[q] * (p.p0[q][e] + at * w.b_ve[e]);
       }
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        e4[q] = ld4(ve + tok[q] * kD + c);
-        g[q] = gate[(int64_t)(row0 + q) * kH + (c >> 6)];
-        at[q] = nr ? s * nr[off_ve + tok[q]] : 0.f;
-      }
-      const f32x4 b = nr ? ld4(nr + off_ve + Vp + c) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < R; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[q][e] += g[q] * (e4[q][e] + at[q] * b[e]);
     }
 #pragma unroll
     for (int q = 0; q < R; ++q) st_bf16x4(out + (int64_t)(row0 + q) * kQKV + n0 + 4 * lane, v[q]);
@@ -262,32 +290,48 @@ struct EpiResid {
   int64_t off;      // noise offset of the parameter's a
   const float* xb;  // [M, nxb] partial dots, summed
   int nxb;
-  template <int R>
-  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, f32x4 (&v)[R]) const {
-    const int m = mb.member(row0);
-    const float* nr = mb.nrow(m);
-    f32x4 xv[R];
+  struct Wave {
+    int row_base;
+    const float* nr;
+    float s, d;
+    f32x4 a;
+  };
+  struct Pre {
+    f32x4 xv[kEpiRows];
+  };
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+    const int m = mb.member(row_base);
+    w.row_base = row_base;
+    w.nr = mb.nrow(m);
+    w.s = 0.f; w.d = 0.f;
+    w.a = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (w.nr) {
+      w.s = mb.sgn(m);
+      w.a = ld4(w.nr + off + n0 + 4 * lane);
+      for (int p = 0; p < nxb; ++p) w.d += xb[(int64_t)(row_base + lane) * nxb + p];
+    }
+  }
+  __device__ __forceinline__ void load(int row0, int n0, int lane, const Wave&, Pre& p) const {
 #pragma unroll
-    for (int q = 0; q < R; ++q) xv[q] = ld4(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane);
-    if (nr) {
-      const float s = mb.sgn(m);
-      const f32x4 a = ld4(nr + off + n0 + 4 * lane);
-      float d[R];
+    for (int q = 0; q < kEpiRows; ++q) p.xv[q] = ld4(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane);
+  }
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, const Wave& w, const Pre& p,
+                                       f32x4 (&v)[R]) const {
+    if (w.nr) {
 #pragma unroll
       for (int q = 0; q < R; ++q) {
-        d[q] = 0.f;
-        for (int p = 0; p < nxb; ++p) d[q] += xb[(int64_t)(row0 + q) * nxb + p];
+        const float d = lane_val(w.d, row0 - w.row_base + q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[q][e] += w.s * d * w.a[e];
       }
-#pragma unroll
-      for (int q = 0; q < R; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[q][e] += s * d[q] * a[e];
     }
 #pragma unroll
     for (int q = 0; q < R; ++q) {
+      f32x4 xv = p.xv[q];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xv[q][e] += v[q][e];
-      *(f32x4*)(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane) = xv[q];
+      for (int e = 0; e < 4; ++e) xv[e] += v[q][e];
+      *(f32x4*)(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane) = xv;
     }
   }
 };
@@ -304,20 +348,37 @@ struct EpiReluSq {
   int64_t off_next_b;   // noise offset of the next linear's b (its input is this output)
   float* xb_next;       // [M, n_tiles]
   int n_tiles;
+  struct Wave {
+    int row_base;
+    const float* nr;
+    float s, xb;
+    f32x4 a, b;
+  };
+  struct Pre {};
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+    const int m = mb.member(row_base);
+    w.row_base = row_base;
+    w.nr = mb.nrow(m);
+    w.s = 0.f; w.xb = 0.f;
+    w.a = w.b = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (w.nr) {
+      w.s = mb.sgn(m);
+      w.a = ld4(w.nr + off + n0 + 4 * lane);
+      w.b = ld4(w.nr + off_next_b + n0 + 4 * lane);
+      w.xb = xb[(int64_t)(row_base + lane) * xb_ld];
+    }
+  }
+  __device__ __forceinline__ void load(int, int, int, const Wave&, Pre&) const {}
   template <int R>
-  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, f32x4 (&v)[R]) const {
-    const int m = mb.member(row0);
-    const float* nr = mb.nrow(m);
-    if (nr) {
-      const float s = mb.sgn(m);
-      const f32x4 a = ld4(nr + off + n0 + 4 * lane);
-      float k[R];
+  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, const Wave& w, const Pre&,
+                                       f32x4 (&v)[R]) const {
+    if (w.nr) {
 #pragma unroll
-      for (int q = 0; q < R; ++q) k[q] = xb[(int64_t)(row0 + q) * xb_ld];
+      for (int q = 0; q < R; ++q) {
+        const float k = lane_val(w.xb, row0 - w.row_base + q);
 #pragma unroll
-      for (int q = 0; q < R; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[q][e] += s * k[q] * a[e];
+        for (int e = 0; e < 4; ++e) v[q][e] += w.s * k * w.a[e];
+      }
     }
 #pragma unroll
     for (int q = 0; q < R; ++q) {
@@ -328,14 +389,13 @@ struct EpiReluSq {
       }
       st_bf16x4(out + (int64_t)(row0 + q) * ldo + n0 + 4 * lane, v[q]);
     }
-    if (nr) {
+    if (w.nr) {
       static_assert(R == 8, "warp_sum8 reduces 8 rows");
-      const f32x4 b = ld4(nr + off_next_b + n0 + 4 * lane);
       float d[R];
 #pragma unroll
       for (int q = 0; q < R; ++q) {
         const f32x4 hv = bf16_round4(v[q]);
-        d[q] = hv[0] * b[0] + hv[1] * b[1] + hv[2] * b[2] + hv[3] * b[3];
+        d[q] = hv[0] * w.b[0] + hv[1] * w.b[1] + hv[2] * w.b[2] + hv[3] * w.b[3];
       }
       const float tot = warp_sum8(d, lane);
       if ((lane & 7) == 0) xb_next[(int64_t)(row0 + (lane >> 3)) * n_tiles + n_tile] = tot;
@@ -356,31 +416,47 @@ struct EpiHeadCE {
   float* tgt_logit;   // [M]
   const int64_t* targets;  // [n_seq, T]
   float* logits;      // [M, vocab] or NULL
+  struct Wave {
+    int row_base, tg;  // tg: the lane's row's target, -1 when it is no column index
+    const float* nr;
+    float s, xb;
+    f32x4 a;
+  };
+  struct Pre {};
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+    const int m = mb.member(row_base);
+    w.row_base = row_base;
+    const int64_t t = targets[(int64_t)mb.seq[m] * mb.T + (row_base - m * mb.T) + lane];
+    w.tg = (t >= 0 && t < vocab) ? (int)t : -1;
+    w.nr = mb.nrow(m);
+    w.s = 0.f; w.xb = 0.f;
+    w.a = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (w.nr) {
+      w.s = mb.sgn(m);
+      w.a = ld4(w.nr + off + n0 + 4 * lane);
+      w.xb = xb[(int64_t)(row_base + lane) * xb_ld];
+    }
+  }
+  __device__ __forceinline__ void load(int, int, int, const Wave&, Pre&) const {}
   template <int R>
-  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, f32x4 (&v)[R]) const {
-    const int m = mb.member(row0);
-    const float* nr = mb.nrow(m);
+  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, const Wave& w, const Pre&,
+                                       f32x4 (&v)[R]) const {
     const int c0 = n0 + 4 * lane;
-    const int64_t* tgrow = targets + (int64_t)mb.seq[m] * mb.T + (row0 - m * mb.T);
-    int64_t tg[R];
+    const int i0 = row0 - w.row_base;
+    if (w.nr) {
 #pragma unroll
-    for (int q = 0; q < R; ++q) tg[q] = tgrow[q];
-    if (nr) {
-      const float s = mb.sgn(m);
-      const f32x4 a = ld4(nr + off + c0);
-      float k[R];
+      for (int q = 0; q < R; ++q) {
+        const float k = lane_val(w.xb, i0 + q);
 #pragma unroll
-      for (int q = 0; q < R; ++q) k[q] = xb[(int64_t)(row0 + q) * xb_ld];
-#pragma unroll
-      for (int q = 0; q < R; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[q][e] += s * k[q] * a[e];
+        for (int e = 0; e < 4; ++e) v[q][e] += w.s * k * w.a[e];
+      }
     }
     static_assert(R == 8, "warp_sum8 reduces 8 rows");
     float se[R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
       const int row = row0 + q;
+      const int tg = lane_val(w.tg, i0 + q);
       se[q] = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -389,7 +465,7 @@ struct EpiHeadCE {
         const float z = 15.0f - 30.0f * fast_rcp(e2 + 1.0f);
         if (c0 + e < vocab) {
           se[q] += fast_exp2((z - 15.0f) * kLog2e);
-          if (tg[q] == c0 + e) tgt_logit[row] = z;
+          if (tg == c0 + e) tgt_logit[row] = z;
           if (logits) logits[(int64_t)row * vocab + c0 + e] = z;
         }
       }

@@ -184,8 +184,11 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
 
   // Epilogue through LDS. The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul
   // output, to which it then adds its fp32 rank-1 term -- and staged as the whole 256 x 256 tile. Each wave then takes
-  // 64 rows in groups of kEpiRows (lane l holds columns 4l .. 4l+3) and hands a group to the epilogue, which issues
-  // all of the group's loads before it computes and stores. Rows past M are skipped.
+  // 64 rows (one member's: M and the member length are multiples of 64) in 8 groups of kEpiRows, lane l holding
+  // columns 4l .. 4l+3. The epilogue functor provides
+  //   begin(row_base, n0, lane, Wave&)           loads made once per wave (noise vectors, per-row scalars by lane),
+  //   load(row0, n0, lane, const Wave&, Pre&)     the per-row data of one group (issued a group ahead),
+  //   rows<R>(row0, n0, n_tile, lane, const Wave&, const Pre&, v)  the group's arithmetic and stores.
   static_assert(S::BN == 256 && S::kThreads == 256 && S::BM == 256, "row epilogue: 256 x 256 tiles, 4 waves");
   bf16_t* st = (bf16_t*)smem_raw;
 #pragma unroll
@@ -198,19 +201,37 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
         st[lr * S::kEpiLd + wn * S::WTN + j * 32 + (lane & 31)] = f32_to_bf16(acc[i][j][r]);
       }
   __syncthreads();
-  constexpr int R = kEpiRows;
-#pragma unroll 1
-  for (int g = 0; g < 64 / R; ++g) {
-    const int lr0 = wave * 64 + g * R;
-    if (m0 + lr0 >= M) break;  // M % 8 == 0: a group is all valid or all past the end
-    f32x4 v[R];
+  constexpr int R = kEpiRows, G = 64 / kEpiRows;
+  static_assert(G % 2 == 0, "groups are processed in pairs");
+  const int row_base = m0 + wave * 64;
+  if (row_base >= M) return;
+  auto tile_rows = [&](int g, f32x4 (&v)[R]) {
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-      const u32x2 p = *(const u32x2*)(st + (lr0 + k) * S::kEpiLd + 4 * lane);
+      const u32x2 p = *(const u32x2*)(st + (wave * 64 + g * R + k) * S::kEpiLd + 4 * lane);
       v[k] = f32x4{__uint_as_float(p[0] << 16), __uint_as_float(p[0] & 0xFFFF0000u), __uint_as_float(p[1] << 16),
                    __uint_as_float(p[1] & 0xFFFF0000u)};
     }
-    epi.template rows<R>(m0 + lr0, n0, n_tile, lane, v);
+  };
+  typename Epi::Wave w;
+  epi.begin(row_base, n0, lane, w);
+  typename Epi::Pre p0, p1;
+  epi.load(row_base, n0, lane, w, p0);
+#pragma unroll 1
+  for (int g = 0; g < G; g += 2) {
+    const int r0 = row_base + g * R;
+    epi.load(r0 + R, n0, lane, w, p1);
+    {
+      f32x4 v[R];
+      tile_rows(g, v);
+      epi.template rows<R>(r0, n0, n_tile, lane, w, p0, v);
+    }
+    if (g + 2 < G) epi.load(r0 + 2 * R, n0, lane, w, p0);
+    {
+      f32x4 v[R];
+      tile_rows(g + 1, v);
+      epi.template rows<R>(r0 + R, n0, n_tile, lane, w, p1, v);
+    }
   }
 }
 

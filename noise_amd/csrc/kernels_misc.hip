@@ -19,20 +19,31 @@ struct EpiLowrank {
   int64_t ldy;
   float* part;        // [M, n_tiles] or NULL
   int n_tiles;
+  struct Wave {
+    int row_base;
+    float k;  // the lane's row's s_m u[row]
+    f32x4 a;
+  };
+  struct Pre {};
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+    const int m = row_base / T;
+    w.row_base = row_base;
+    w.a = *(const f32x4*)(noise + (int64_t)m * stride + a_off + n0 + 4 * lane);
+    w.k = sign[m] * u[row_base + lane];
+  }
+  __device__ __forceinline__ void load(int, int, int, const Wave&, Pre&) const {}
   template <int R>
-  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, f32x4 (&v)[R]) const {
-    const int m = row0 / T;
-    const f32x4 a = *(const f32x4*)(noise + (int64_t)m * stride + a_off + n0 + 4 * lane);
+  __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, const Wave& w, const Pre&,
+                                       f32x4 (&v)[R]) const {
     static_assert(R == 8, "warp_sum8 reduces 8 rows");
-    float k[R], ss[R];
-#pragma unroll
-    for (int q = 0; q < R; ++q) k[q] = sign[m] * u[row0 + q];
+    float ss[R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
+      const float k = lane_val(w.k, row0 - w.row_base + q);
       ss[q] = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[q][e] += k[q] * a[e];
+        v[q][e] += k * w.a[e];
         ss[q] += v[q][e] * v[q][e];
       }
       if (y) *(f32x4*)(y + (int64_t)(row0 + q) * ldy + n0 + 4 * lane) = v[q];
