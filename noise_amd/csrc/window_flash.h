@@ -158,32 +158,47 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
   i_begin = i_begin / kFlashBI * kFlashBI;
 
   const float* lse_in = (MODE == kCredit) ? a.lse_in + ((int64_t)b * a.heads + head) * T : nullptr;
-  const bf16_t* vgb = (MODE == kAttn || MODE == kCenter) ? (const bf16_t*)a.v + b * a.v_sb + head * 64 : nullptr;
-  const float* vgf = (MODE == kCredit) ? (const float*)a.v + b * a.v_sb + head * 64 : nullptr;
   const int kg = tid >> 4, dg = tid & 15;  // V staging: inputs 4 kg .. 4 kg + 3, channels 4 dg .. 4 dg + 3
+
+  // Tile loads through buffer resources over this row's inputs: per-lane offsets are fixed, the tile's first input
+  // goes in the scalar offset. y (and kCenter's values) as 64 rows x 8 16-byte chunks, 2 per thread; kAttn / kCredit
+  // values as 4 inputs x 4 channels per thread.
+  constexpr bool kVRows = (MODE == kCenter);
+  constexpr int kVElt = (MODE == kCredit) ? 4 : 2;  // bytes per value element
+  const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)yg, 0, (int)(((int64_t)(T - 1) * a.y_st + 64) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const char*)a.v + (b * a.v_sb + head * 64) * kVElt), 0,
+      (MODE == kLse) ? 0 : (int)(((int64_t)(T - 1) * a.v_st + 64) * kVElt), 0x00020000);
+  const int y_step = (int)a.y_st * 2, v_step = (int)a.v_st * kVElt;  // bytes per input
+  int y_vo[2], v_vo[4];
+#pragma unroll
+  for (int rep = 0; rep < 2; ++rep) {
+    const int v = tid + rep * 256;
+    y_vo[rep] = ((v >> 3) * (int)a.y_st + (v & 7) * 8) * 2;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    v_vo[k] = kVRows ? (k < 2 ? (((tid + k * 256) >> 3) * (int)a.v_st + ((tid + k * 256) & 7) * 8) * 2 : 0)
+                     : ((4 * kg + k) * (int)a.v_st + 4 * dg) * kVElt;
 
   auto load = [&](int i0, FlashStage<MODE>& st) {
 #pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-      const int v = tid + rep * 256;
-      st.y[rep] = *(const u32x4*)(yg + (int64_t)(i0 + (v >> 3)) * a.y_st + (v & 7) * 8);
-    }
+    for (int rep = 0; rep < 2; ++rep)
+      st.y[rep] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(y_rsrc, y_vo[rep], i0 * y_step, 0));
     if constexpr (MODE == kAttn) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        st.v[k] = *(const u32x2*)(vgb + (int64_t)(i0 + 4 * kg + k) * a.v_st + 4 * dg);
-      }
+      for (int k = 0; k < 4; ++k)
+        st.v[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(v_rsrc, v_vo[k], i0 * v_step, 0));
     } else if constexpr (MODE == kCredit) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        st.v[k] = *(const f32x4*)(vgf + (int64_t)(i0 + 4 * kg + k) * a.v_st + 4 * dg);
+        st.v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_vo[k], i0 * v_step, 0));
       st.lse = (tid < 64) ? lse_in[i0 + tid] : 0.f;
     } else if constexpr (MODE == kCenter) {
 #pragma unroll
-      for (int rep = 0; rep < 2; ++rep) {
-        const int v = tid + rep * 256;
-        st.v[rep] = *(const u32x4*)(vgb + (int64_t)(i0 + (v >> 3)) * a.v_st + (v & 7) * 8);
-      }
+      for (int rep = 0; rep < 2; ++rep)
+        st.v[rep] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_vo[rep], i0 * v_step, 0));
     }
   };
   auto store = [&](int s, const FlashStage<MODE>& st) {
@@ -294,21 +309,28 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
         }
       }
 
-      // ---- probabilities ----
+      // ---- probabilities: masked pairs of a partial tile get -inf first, so exp2 runs unconditionally ----
 #pragma unroll
       for (int og = 0; og < OG; ++og) {
         if (!any[og]) continue;
         const int my_o = ow + og * 32 + col;
+        if (!full[og]) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int i = i0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+              const int lag = (MODE == kCredit) ? i - my_o : my_o - i;
+              sc[og][t][r] = (lag >= 0 && lag <= W) ? sc[og][t][r] : -INFINITY;
+            }
+        }
         if (MODE == kCredit) {
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int il = t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-              const int i = i0 + il;
-              const bool ok = full[og] || ((i - my_o) >= 0 && (i - my_o) <= W);
-              const float e = fast_exp2(sc[og][t][r] * qk_scale - lse_s[s][il] * kLog2e);
-              sc[og][t][r] = ok ? e : 0.f;
+              sc[og][t][r] = fast_exp2(sc[og][t][r] * qk_scale - lse_s[s][il] * kLog2e);
             }
         } else if (bounded) {
           float ls = 0.f;
@@ -316,9 +338,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int i = i0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-              const bool ok = full[og] || ((my_o - i) >= 0 && (my_o - i) <= W);
-              const float p = ok ? fast_exp2(sc[og][t][r] * qk_scale - ref) : 0.f;
+              const float p = fast_exp2(sc[og][t][r] * qk_scale - ref);
               sc[og][t][r] = p;
               ls += p;
             }
@@ -329,9 +349,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int i = i0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-              const bool ok = full[og] || ((my_o - i) >= 0 && (my_o - i) <= W);
-              const float e = ok ? sc[og][t][r] * qk_scale : -INFINITY;
+              const float e = sc[og][t][r] * qk_scale;
               sc[og][t][r] = e;
               mt = fmaxf(mt, e);
             }
