@@ -157,6 +157,37 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
   }
 }
 
+// gate[r, hd] = 2 sigmoid(h[r, :32] . W_g[hd] + s (h[r, :32] . b_g) a_g[hd]) (eggroll.py:85-89), for a block with
+// value embeddings whose h comes from a GEMM epilogue; 8 lanes per row, lane hd of the row computes head hd. The
+// channel sums go in chunks of 8 combined pairwise, as in mix_norm_kernel.
+__global__ __launch_bounds__(256) void gate_kernel(Members mb, const bf16_t* __restrict__ h,
+                                                   const float* __restrict__ w_gate, int64_t off_gate,
+                                                   float* __restrict__ gate, int64_t M) {
+  const int64_t r = blockIdx.x * 32 + (threadIdx.x >> 3);
+  if (r >= M) return;
+  const int hd = threadIdx.x & 7;
+  const int m = mb.member(r);
+  const float* nr = mb.nrow(m);
+  const float s = mb.sgn(m);
+  float g[4], db[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const u32x4 p = *(const u32x4*)(h + r * kD + 8 * c);
+    float hv[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { hv[2 * j] = __uint_as_float(p[j] << 16); hv[2 * j + 1] = __uint_as_float(p[j] & 0xFFFF0000u); }
+    g[c] = 0.f; db[c] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g[c] += hv[j] * w_gate[hd * kGateIn + 8 * c + j];
+      if (nr) db[c] += hv[j] * nr[off_gate + kH + 8 * c + j];
+    }
+  }
+  float pre = (g[0] + g[1]) + (g[2] + g[3]);
+  if (nr) pre += s * ((db[0] + db[1]) + (db[2] + db[3])) * nr[off_gate + hd];
+  gate[r * kH + hd] = 2.0f / (1.0f + expf(-pre));
+}
+
 // GEMM epilogues. The GEMM hands over one output row per wave: lane l holds columns n0 + 4l .. n0 + 4l + 3 of the
 // workgroup's 256-column tile. Noise rows are 16-byte aligned and every parameter slice starts at a multiple of 4.
 
@@ -282,56 +313,124 @@ struct EpiQKV {
   }
 };
 
-// x[row, col] += acc + s (sum of the xb partials) a[col]   (the residual adds of utils/model.py:118-119)
-struct EpiResid {
+// x += acc + s (sum of the xb partials) a (the residual adds of utils/model.py:118-119); with `mix`, then the next
+// block's lambda mix x = (l_r + s eps_r) x + (l_0 + s eps_0) x0 (eggroll.py:77-79); x is written back, and
+// h = norm(x) in bf16 (utils/model.py:46-47) with the dots h . b_k of the next linear's rank-1 terms. The tile holds
+// whole 512-wide rows (128 x 512 tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3.
+struct EpiResidNorm {
   Members mb;
-  float* x;
-  int64_t ldx;
-  int64_t off;      // noise offset of the parameter's a
-  const float* xb;  // [M, nxb] partial dots, summed
+  float* x;             // [M, 512] residual stream, read and written
+  const float* xbp;     // [M, nxb] partial dots of this linear's input with its b
   int nxb;
+  int64_t off;          // noise offset of this linear's a
+  int mix;
+  const float* x0;      // [M, 512] (mix only)
+  const float* resid_lambdas;
+  const float* x0_lambdas;
+  int layer;            // the block whose lambdas mix
+  int64_t off_resid, off_x0;
+  bf16_t* h;            // [M, 512]
+  int ndot;
+  int64_t off_b[3];     // noise offsets of the next linear's b vectors
+  float* xb;            // [M, 4]
   struct Wave {
     int row_base;
     const float* nr;
-    float s, d;
-    f32x4 a;
+    float s, d, lr, l0;
+    f32x4 a[2], b[3][2];
   };
   struct Pre {
-    f32x4 xv[kEpiRows];
+    f32x4 xv[kEpiRows][2], x0v[kEpiRows][2];
   };
-  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+  __device__ __forceinline__ void begin(int row_base, int, int lane, Wave& w) const {
     const int m = mb.member(row_base);
     w.row_base = row_base;
     w.nr = mb.nrow(m);
-    w.s = 0.f; w.d = 0.f;
-    w.a = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (w.nr) {
-      w.s = mb.sgn(m);
-      w.a = ld4(w.nr + off + n0 + 4 * lane);
-      for (int p = 0; p < nxb; ++p) w.d += xb[(int64_t)(row_base + lane) * nxb + p];
+    w.s = mb.sgn(m);
+    w.d = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      w.a[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 3; ++k) w.b[k][hh] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  }
-  __device__ __forceinline__ void load(int row0, int n0, int lane, const Wave&, Pre& p) const {
-#pragma unroll
-    for (int q = 0; q < kEpiRows; ++q) p.xv[q] = ld4(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane);
-  }
-  template <int R>
-  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, const Wave& w, const Pre& p,
-                                       f32x4 (&v)[R]) const {
     if (w.nr) {
+      for (int p = 0; p < nxb; ++p) w.d += xbp[(int64_t)(row_base + lane) * nxb + p];
 #pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const float d = lane_val(w.d, row0 - w.row_base + q);
+      for (int hh = 0; hh < 2; ++hh) {
+        w.a[hh] = ld4(w.nr + off + hh * 256 + 4 * lane);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[q][e] += w.s * d * w.a[e];
+        for (int k = 0; k < 3; ++k)
+          if (k < ndot) w.b[k][hh] = ld4(w.nr + off_b[k] + hh * 256 + 4 * lane);
       }
     }
+    w.lr = 1.f; w.l0 = 0.f;
+    if (mix) {
+      w.lr = resid_lambdas[layer];
+      w.l0 = x0_lambdas[layer];
+      if (w.nr) { w.lr += w.s * w.nr[off_resid + layer]; w.l0 += w.s * w.nr[off_x0 + layer]; }
+    }
+  }
+  __device__ __forceinline__ void load(int row0, int, int lane, const Wave&, Pre& p) const {
+#pragma unroll
+    for (int q = 0; q < kEpiRows; ++q)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        p.xv[q][hh] = ld4(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
+        if (mix) p.x0v[q][hh] = ld4(x0 + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
+      }
+  }
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int, int, int lane, const Wave& w, const Pre& p,
+                                       f32x4 (&v)[R][2]) const {
+    static_assert(R == 8, "warp_sum8 reduces 8 rows");
+    const int i0 = row0 - w.row_base;
+    float ss[R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      f32x4 xv = p.xv[q];
+      const float d = w.nr ? lane_val(w.d, i0 + q) : 0.f;
+      ss[q] = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xv[e] += v[q][e];
-      *(f32x4*)(x + (int64_t)(row0 + q) * ldx + n0 + 4 * lane) = xv;
+      for (int hh = 0; hh < 2; ++hh) {
+        f32x4 xn = p.xv[q][hh];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float val = v[q][hh][e];
+          if (w.nr) val += w.s * d * w.a[hh][e];
+          xn[e] += val;
+          if (mix) xn[e] = w.lr * xn[e] + w.l0 * p.x0v[q][hh][e];
+          ss[q] += xn[e] * xn[e];
+        }
+        v[q][hh] = xn;
+        *(f32x4*)(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane) = xn;
+      }
+    }
+    const float tot = warp_sum8(ss, lane);
+    float dk[3][R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const float inv = rsqrtf(lane_val(tot, 8 * q) * (1.0f / kD) + kNormEps);
+#pragma unroll
+      for (int k = 0; k < 3; ++k) dk[k][q] = 0.f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        f32x4 hv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hv[e] = bf16_to_f32(f32_to_bf16(v[q][hh][e] * inv));
+        st_bf16x4(h + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane, hv);
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dk[k][q] += hv[e] * w.b[k][hh][e];
+      }
+    }
+    if (w.nr) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        if (k >= ndot) break;
+        const float dt = warp_sum8(dk[k], lane);
+        if ((lane & 7) == 0) xb[(int64_t)(row0 + (lane >> 3)) * 4 + k] = dt;
+      }
     }
   }
 };
@@ -506,6 +605,7 @@ __global__ __launch_bounds__(256) void member_sum_kernel(const float* __restrict
 }
 
 using Tile = GemmShape<256, 256, 32, 2, 2>;
+using RowTile = GemmShape<128, 512, 32, 1, 4>;  // whole 512-wide rows, for the epilogues that normalize
 constexpr int kAttnOG = 1;  // 32 outputs per wave (2 waves per SIMD)
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -545,7 +645,7 @@ static bool g_prepared = false;
 static int prepare_all() {
   if (g_prepared) return NOISE_OK;
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiQKV>()));
-  NOISE_CHECK_HIP((prepare_gemm<Tile, EpiResid>()));
+  NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiReluSq>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiHeadCE>()));
   g_prepared = true;
@@ -603,18 +703,24 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     NOISE_REQUIRE(L.w_qkv && L.w_proj && L.w_fc && L.w_mlp_proj, "layer %d weight pointer is NULL", i);
     NOISE_REQUIRE((L.w_gate == nullptr) == (L.ve == nullptr), "layer %d: w_gate and ve must both be set or both NULL", i);
     NOISE_REQUIRE(L.window >= 0, "layer %d: negative window", i);
-    // lambda mix + norm + q/k/v dots + gate
-    NormArgs na;
-    memset(&na, 0, sizeof(na));
-    na.x = ws.x; na.x0 = ws.x0; na.mix = 1; na.first = (i == 0);
-    na.resid_lambdas = model->resid_lambdas; na.x0_lambdas = model->x0_lambdas; na.layer = i;
-    na.off_resid = pert->resid_lambdas; na.off_x0 = pert->x0_lambdas;
-    na.h = ws.h; na.ndot = 3;
-    na.off_b[0] = pert->c_q[i] + kD; na.off_b[1] = pert->c_k[i] + kD; na.off_b[2] = pert->c_v[i] + kD;
-    na.xb = ws.xb; na.w_gate = L.w_gate; na.off_gate = pert->ve_gate[i]; na.gate = ws.gate; na.M = M;
-    {
+    if (i == 0) {
+      // lambda mix + norm + q/k/v dots + gate of the first block (later blocks get theirs from the epilogue of the
+      // previous block's MLP projection)
+      NormArgs na;
+      memset(&na, 0, sizeof(na));
+      na.x = ws.x; na.x0 = ws.x0; na.mix = 1; na.first = 1;
+      na.resid_lambdas = model->resid_lambdas; na.x0_lambdas = model->x0_lambdas; na.layer = 0;
+      na.off_resid = pert->resid_lambdas; na.off_x0 = pert->x0_lambdas;
+      na.h = ws.h; na.ndot = 3;
+      na.off_b[0] = pert->c_q[0] + kD; na.off_b[1] = pert->c_k[0] + kD; na.off_b[2] = pert->c_v[0] + kD;
+      na.xb = ws.xb; na.w_gate = L.w_gate; na.off_gate = pert->ve_gate[0]; na.gate = ws.gate; na.M = M;
       NoiseTimer tm(kTimeNorm, stream);
       hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, na);
+      NOISE_LAUNCH_CHECK();
+    } else if (L.w_gate) {
+      NoiseTimer tm(kTimeNorm, stream);
+      hipLaunchKernelGGL(gate_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), 0, stream, mb, ws.h, L.w_gate,
+                         pert->ve_gate[i], ws.gate, M);
       NOISE_LAUNCH_CHECK();
     }
 
@@ -640,20 +746,15 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
       NOISE_CHECK_HIP((launch_flash<kAttn, true, kAttnOG>(fa, members, kH, stream)));
     }
 
-    EpiResid ep{mb, ws.x, kD, pert->c_proj[i], ws.xbp, kH};
+    // attention projection + residual, then the MLP's norm and c_fc's rank-1 dot
+    EpiResidNorm ep;
+    memset(&ep, 0, sizeof(ep));
+    ep.mb = mb; ep.x = ws.x; ep.xbp = ws.xbp; ep.nxb = kH; ep.off = pert->c_proj[i];
+    ep.h = ws.h; ep.ndot = 1; ep.off_b[0] = pert->c_fc[i] + kF;  // c_fc's a spans its 2048 outputs
+    ep.xb = ws.xb;
     {
       NoiseTimer tm(kTimeProj, stream);
-      NOISE_CHECK_HIP((launch_gemm<Tile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
-    }
-
-    NormArgs nb;
-    memset(&nb, 0, sizeof(nb));
-    nb.x = ws.x; nb.h = ws.h; nb.ndot = 1; nb.off_b[0] = pert->c_fc[i] + kF;  // c_fc's a spans its 2048 outputs
-    nb.xb = ws.xb; nb.M = M;
-    {
-      NoiseTimer tm(kTimeNorm, stream);
-      hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nb);
-      NOISE_LAUNCH_CHECK();
+      NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
     }
 
     EpiReluSq er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4, pert->mlp_proj[i] + kD, ws.xb1, kF / Tile::BN};
@@ -661,20 +762,26 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
       NoiseTimer tm(kTimeFc, stream);
       NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
     }
-    EpiResid em{mb, ws.x, kD, pert->mlp_proj[i], ws.xb1, kF / Tile::BN};
+
+    // MLP projection + residual, then the next block's lambda mix, norm and q/k/v dots (or the final norm and
+    // lm_head's rank-1 dot)
+    const bool last = i + 1 == model->n_layer;
+    EpiResidNorm em;
+    memset(&em, 0, sizeof(em));
+    em.mb = mb; em.x = ws.x; em.xbp = ws.xb1; em.nxb = kF / Tile::BN; em.off = pert->mlp_proj[i];
+    em.h = ws.h; em.xb = ws.xb;
+    if (last) {
+      em.ndot = 1; em.off_b[0] = pert->lm_head + Vp;
+    } else {
+      em.mix = 1; em.x0 = ws.x0; em.resid_lambdas = model->resid_lambdas; em.x0_lambdas = model->x0_lambdas;
+      em.layer = i + 1; em.off_resid = pert->resid_lambdas; em.off_x0 = pert->x0_lambdas;
+      em.ndot = 3;
+      em.off_b[0] = pert->c_q[i + 1] + kD; em.off_b[1] = pert->c_k[i + 1] + kD; em.off_b[2] = pert->c_v[i + 1] + kD;
+    }
     {
       NoiseTimer tm(kTimeMlpProj, stream);
-      NOISE_CHECK_HIP((launch_gemm<Tile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+      NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
     }
-  }
-
-  NormArgs nf;
-  memset(&nf, 0, sizeof(nf));
-  nf.x = ws.x; nf.h = ws.h; nf.ndot = 1; nf.off_b[0] = pert->lm_head + Vp; nf.xb = ws.xb; nf.M = M;
-  {
-    NoiseTimer tm(kTimeNorm, stream);
-    hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, nf);
-    NOISE_LAUNCH_CHECK();
   }
 
   const int n_part = Vp / Tile::BN;

@@ -2,8 +2,8 @@
 // the x @ weight.t() of nn.Linear weights stored [out, in]). The accumulator tile goes to an epilogue functor, which
 // is where the population-specific work (rank-1 member corrections, residual adds, relu^2, soft-capped CE) happens.
 //
-// Tiling: a workgroup computes 256 x 256 with 2 x 2 waves; a wave owns 128 x 128 as 4 x 4 MFMA tiles
-// (v_mfma_f32_32x32x16_bf16). K advances in steps of 32 through kStages LDS stages filled by direct-to-LDS buffer
+// Tiling: a workgroup computes 256 x 256 with 2 x 2 waves, or 128 x 512 with 1 x 4 waves (whole 512-wide rows, for
+// epilogues that normalize rows); a wave owns 128 x 128 as 4 x 4 MFMA tiles (v_mfma_f32_32x32x16_bf16). K advances in steps of 32 through kStages LDS stages filled by direct-to-LDS buffer
 // loads (buffer_load_dwordx4 ... lds): the loads of step kt + kStages are issued as soon as every wave is done with
 // step kt, so up to three steps of loads are in flight behind the MFMAs and no register holds staged data.
 // One barrier per step, placed between the step's two 16-deep k-substeps: the second k-substep's fragments are
@@ -31,22 +31,43 @@ struct GemmShape {
   static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
   static constexpr int kStages = 4;
   static constexpr int kStageBytes = (BM + BN) * BK * 2;  // A rows then B rows
+  static constexpr int kADma = BM / 64, kBDma = BN / 64;  // 1 KB direct-to-LDS loads per wave and step
+  static constexpr int kDma = kADma + kBDma;
   static constexpr int kEpiLd = BN + 16;                  // bf16 staging row stride (16 elements of padding)
   static constexpr int kMainLds = kStages * kStageBytes;
   static constexpr int kEpiLds = BM * kEpiLd * 2;         // the whole tile in bf16
   static constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
-  static_assert(BM == 256 && BN == 256 && BK == 32 && WM == 2 && WN == 2, "the main loop is written for 256x256x32");
+  static constexpr int kWaveRows = BM / 4;                // epilogue rows per wave
+  static_assert(BK == 32 && WTM == 128 && WTN == 128 && kThreads == 256, "main loop: 4 waves of 128x128, K steps of 32");
+  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 512), "tiles: 256x256 or 128x512");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// s_waitcnt vmcnt(n) for n in {0, 8, 16, 24}, expcnt and lgkmcnt left alone (gfx9 encoding: vmcnt bits 3:0 and
-// 15:14, expcnt 6:4, lgkmcnt 11:8).
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  if (n >= 24) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8) | (1 << 14));
-  else if (n >= 16) __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8) | (1 << 14));
-  else if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));
-  else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+// One 16-byte-per-lane direct-to-LDS buffer load (buffer_load_dwordx4 ... lds): lane l's 16 bytes land at
+// lds + 16 l. The builtin is a gfx950 target builtin, so it is only spelled out in the device pass (the host pass
+// also checks kernel template bodies and rejects it).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds, int voff, int soff) {
+#if __HIP_DEVICE_COMPILE__
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
+#endif
+}
+
+// s_waitcnt vmcnt(n) with expcnt and lgkmcnt left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8); n < 64.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_imm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// Wait until at most `steps` K steps of kDma loads each are still in flight (steps in 0 .. 3).
+template <int kDma>
+__device__ __forceinline__ void wait_steps(int steps) {
+  if (steps >= 3) wait_vmcnt_imm<3 * kDma>();
+  else if (steps == 2) wait_vmcnt_imm<2 * kDma>();
+  else if (steps == 1) wait_vmcnt_imm<kDma>();
+  else wait_vmcnt_imm<0>();
 }
 constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0)
 
@@ -59,13 +80,56 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Hands a group of rows to the epilogue: f32x4[R] for 256-column tiles, f32x4[R][2] for 512-column tiles.
+template <int H>
+struct EpiRows;
+template <>
+struct EpiRows<1> {
+  template <int R, class Epi>
+  __device__ __forceinline__ static void run(const Epi& epi, int row0, int n0, int n_tile, int lane,
+                                             const typename Epi::Wave& w, const typename Epi::Pre& p,
+                                             f32x4 (&v)[R][1]) {
+    f32x4 v1[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) v1[k] = v[k][0];
+    epi.template rows<R>(row0, n0, n_tile, lane, w, p, v1);
+  }
+};
+template <>
+struct EpiRows<2> {
+  template <int R, class Epi>
+  __device__ __forceinline__ static void run(const Epi& epi, int row0, int n0, int n_tile, int lane,
+                                             const typename Epi::Wave& w, const typename Epi::Pre& p,
+                                             f32x4 (&v)[R][2]) {
+    epi.template rows<R>(row0, n0, n_tile, lane, w, p, v);
+  }
+};
+
+// One group of kEpiRows staged bf16 rows (row stride ld) to the epilogue: lane l takes columns 4l .. 4l+3 of each
+// 256-column half.
+template <int ld, int H, class Epi>
+__device__ __forceinline__ void epi_group(const Epi& epi, const bf16_t* st, int row0, int n0, int n_tile, int lane,
+                                          const typename Epi::Wave& w, const typename Epi::Pre& p) {
+  f32x4 v[kEpiRows][H];
+#pragma unroll
+  for (int k = 0; k < kEpiRows; ++k)
+#pragma unroll
+    for (int hh = 0; hh < H; ++hh) {
+      const u32x2 q = *(const u32x2*)(st + k * ld + hh * 256 + 4 * lane);
+      v[k][hh] = f32x4{__uint_as_float(q[0] << 16), __uint_as_float(q[0] & 0xFFFF0000u), __uint_as_float(q[1] << 16),
+                       __uint_as_float(q[1] & 0xFFFF0000u)};
+    }
+  EpiRows<H>::template run<kEpiRows>(epi, row0, n0, n_tile, lane, w, p, v);
+}
+
 template <class S, class Epi>
 __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __restrict__ A, int64_t lda,
                                                               const bf16_t* __restrict__ B, int64_t ldb, int M, int N,
                                                               int K, Epi epi) {
   constexpr int NS = S::kStages;
+  static_assert(NS == 4, "prologue and waits assume 4 stages");
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  constexpr int kAStage = S::BM * S::BK * 2;  // 16 KB of A rows, then 16 KB of B rows
+  constexpr int kAStage = S::BM * S::BK * 2;  // A rows, then B rows
   constexpr int kStage = S::kStageBytes;
 
   // Workgroups are dispatched round-robin over the 8 XCDs; tiles are renumbered so that each XCD walks a contiguous
@@ -92,26 +156,24 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
       __builtin_amdgcn_make_buffer_rsrc((void*)(B + (int64_t)n0 * ldb), 0, b_rows * (int)ldb * 2, 0x00020000);
 
   // One direct-to-LDS load fills 1 KB = 16 rows x 4 chunks: lane l writes LDS bytes 16 l .. 16 l + 15, i.e. row
-  // l >> 2, slot l & 3, so it fetches global chunk (l & 3) ^ ((l >> 4) & 3). Wave w fills row groups 4 w .. 4 w + 3
-  // of A and of B.
+  // l >> 2, slot l & 3, so it fetches global chunk (l & 3) ^ ((l >> 4) & 3). Wave w fills row groups
+  // w kADma .. (w + 1) kADma - 1 of A and w kBDma .. (w + 1) kBDma - 1 of B.
   const int drow = lane >> 2, dchunk = (lane & 3) ^ ((lane >> 4) & 3);
-  int a_vo[4], b_vo[4];
+  int a_vo[S::kADma], b_vo[S::kBDma];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = (wave * 4 + j) * 16 + drow;
-    a_vo[j] = (r * (int)lda + dchunk * 8) * 2;
-    b_vo[j] = (r * (int)ldb + dchunk * 8) * 2;
-  }
+  for (int j = 0; j < S::kADma; ++j) a_vo[j] = (((wave * S::kADma + j) * 16 + drow) * (int)lda + dchunk * 8) * 2;
+#pragma unroll
+  for (int j = 0; j < S::kBDma; ++j) b_vo[j] = (((wave * S::kBDma + j) * 16 + drow) * (int)ldb + dchunk * 8) * 2;
   auto dma = [&](int kt, int stage) {
     const int koff = kt * S::BK * 2;
-    unsigned char* base = smem_raw + stage * kStage + wave * 4 * 1024;
+    unsigned char* a_base = smem_raw + stage * kStage + wave * S::kADma * 1024;
+    unsigned char* b_base = smem_raw + stage * kStage + kAStage + wave * S::kBDma * 1024;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(base + j * 1024), 16, a_vo[j], koff, 0, 0);
+    for (int j = 0; j < S::kADma; ++j)
+      dma16(a_rsrc, a_base + j * 1024, a_vo[j], koff);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kAStage + j * 1024), 16, b_vo[j], koff, 0,
-                                               0);
+    for (int j = 0; j < S::kBDma; ++j)
+      dma16(b_rsrc, b_base + j * 1024, b_vo[j], koff);
   };
 
   // Fragment offsets: row (lane & 31) of a 32-row tile, chunk 2 kk + (lane >> 5), in slot chunk ^ row bits 2..3.
@@ -139,7 +201,7 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
 #pragma unroll
   for (int s = 0; s < NS; ++s)
     if (s < nk) dma(s, s);
-  wait_vmcnt(8 * min(nk - 1, NS - 1));
+  wait_steps<S::kDma>(min(nk - 1, NS - 1));
   lds_barrier();
   bf16x8 f0a[S::TM], f0b[S::TN], f1a[S::TM], f1b[S::TN];
 #pragma unroll
@@ -163,7 +225,7 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0a[i], f0b[j], acc[i][j], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    wait_vmcnt(8 * max(0, min(nk - 2 - kt, NS - 2)));
+    wait_steps<S::kDma>(max(0, min(nk - 2 - kt, NS - 2)));
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     if (kt + NS < nk) dma(kt + NS, kt % NS);
@@ -183,13 +245,13 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   __syncthreads();  // every wave is done reading the stages before the epilogue reuses the LDS
 
   // Epilogue through LDS. The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul
-  // output, to which it then adds its fp32 rank-1 term -- and staged as the whole 256 x 256 tile. Each wave then takes
-  // 64 rows (one member's: M and the member length are multiples of 64) in 8 groups of kEpiRows, lane l holding
-  // columns 4l .. 4l+3. The epilogue functor provides
+  // output, to which it then adds its fp32 rank-1 term -- and staged as the whole tile. Each wave then takes
+  // kWaveRows rows (one member's: M and the member length are multiples of 64) in groups of kEpiRows; lane l holds
+  // columns 4l .. 4l+3 of each 256-column half. The epilogue functor provides
   //   begin(row_base, n0, lane, Wave&)           loads made once per wave (noise vectors, per-row scalars by lane),
   //   load(row0, n0, lane, const Wave&, Pre&)     the per-row data of one group (issued a group ahead),
-  //   rows<R>(row0, n0, n_tile, lane, const Wave&, const Pre&, v)  the group's arithmetic and stores.
-  static_assert(S::BN == 256 && S::kThreads == 256 && S::BM == 256, "row epilogue: 256 x 256 tiles, 4 waves");
+  //   rows<R>(row0, n0, n_tile, lane, const Wave&, const Pre&, v)  the group's arithmetic and stores, with
+  //   v = f32x4[R] (256-column tiles) or f32x4[R][2] (512-column tiles: columns 4l.. and 256 + 4l..).
   bf16_t* st = (bf16_t*)smem_raw;
 #pragma unroll
   for (int i = 0; i < S::TM; ++i)
@@ -201,37 +263,22 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
         st[lr * S::kEpiLd + wn * S::WTN + j * 32 + (lane & 31)] = f32_to_bf16(acc[i][j][r]);
       }
   __syncthreads();
-  constexpr int R = kEpiRows, G = 64 / kEpiRows;
+  constexpr int R = kEpiRows, G = S::kWaveRows / kEpiRows, H = S::BN / 256;
   static_assert(G % 2 == 0, "groups are processed in pairs");
-  const int row_base = m0 + wave * 64;
+  const int row_base = m0 + wave * S::kWaveRows;
   if (row_base >= M) return;
-  auto tile_rows = [&](int g, f32x4 (&v)[R]) {
-#pragma unroll
-    for (int k = 0; k < R; ++k) {
-      const u32x2 p = *(const u32x2*)(st + (wave * 64 + g * R + k) * S::kEpiLd + 4 * lane);
-      v[k] = f32x4{__uint_as_float(p[0] << 16), __uint_as_float(p[0] & 0xFFFF0000u), __uint_as_float(p[1] << 16),
-                   __uint_as_float(p[1] & 0xFFFF0000u)};
-    }
-  };
   typename Epi::Wave w;
   epi.begin(row_base, n0, lane, w);
   typename Epi::Pre p0, p1;
   epi.load(row_base, n0, lane, w, p0);
+  const bf16_t* st_wave = st + wave * S::kWaveRows * S::kEpiLd;
 #pragma unroll 1
   for (int g = 0; g < G; g += 2) {
     const int r0 = row_base + g * R;
     epi.load(r0 + R, n0, lane, w, p1);
-    {
-      f32x4 v[R];
-      tile_rows(g, v);
-      epi.template rows<R>(r0, n0, n_tile, lane, w, p0, v);
-    }
+    epi_group<S::kEpiLd, H>(epi, st_wave + g * R * S::kEpiLd, r0, n0, n_tile, lane, w, p0);
     if (g + 2 < G) epi.load(r0 + 2 * R, n0, lane, w, p0);
-    {
-      f32x4 v[R];
-      tile_rows(g + 1, v);
-      epi.template rows<R>(r0 + R, n0, n_tile, lane, w, p1, v);
-    }
+    epi_group<S::kEpiLd, H>(epi, st_wave + (g + 1) * R * S::kEpiLd, r0 + R, n0, n_tile, lane, w, p1);
   }
 }
 
