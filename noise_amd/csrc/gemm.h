@@ -61,14 +61,6 @@ __device__ __forceinline__ void wait_vmcnt_imm() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
-// Wait until at most `steps` K steps of kDma loads each are still in flight (steps in 0 .. 3).
-template <int kDma>
-__device__ __forceinline__ void wait_steps(int steps) {
-  if (steps >= 3) wait_vmcnt_imm<3 * kDma>();
-  else if (steps == 2) wait_vmcnt_imm<2 * kDma>();
-  else if (steps == 1) wait_vmcnt_imm<kDma>();
-  else wait_vmcnt_imm<0>();
-}
 constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0)
 
 // Workgroup barrier without a memory fence: the fence of __syncthreads would also wait for every load still in
@@ -164,16 +156,20 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   for (int j = 0; j < S::kADma; ++j) a_vo[j] = (((wave * S::kADma + j) * 16 + drow) * (int)lda + dchunk * 8) * 2;
 #pragma unroll
   for (int j = 0; j < S::kBDma; ++j) b_vo[j] = (((wave * S::kBDma + j) * 16 + drow) * (int)ldb + dchunk * 8) * 2;
+  const int nk = K / S::BK;
+  // Steps past the last one are issued too, with an offset past the buffer's end: the hardware returns zeros
+  // without a memory access, and every step has the same number of loads in flight.
   auto dma = [&](int kt, int stage) {
     const int koff = kt * S::BK * 2;
+    const int oob = kt < nk ? 0 : (1 << 30);
     unsigned char* a_base = smem_raw + stage * kStage + wave * S::kADma * 1024;
     unsigned char* b_base = smem_raw + stage * kStage + kAStage + wave * S::kBDma * 1024;
 #pragma unroll
     for (int j = 0; j < S::kADma; ++j)
-      dma16(a_rsrc, a_base + j * 1024, a_vo[j], koff);
+      dma16(a_rsrc, a_base + j * 1024, a_vo[j] + oob, koff);
 #pragma unroll
     for (int j = 0; j < S::kBDma; ++j)
-      dma16(b_rsrc, b_base + j * 1024, b_vo[j], koff);
+      dma16(b_rsrc, b_base + j * 1024, b_vo[j] + oob, koff);
   };
 
   // Fragment offsets: row (lane & 31) of a 32-row tile, chunk 2 kk + (lane >> 5), in slot chunk ^ row bits 2..3.
@@ -196,12 +192,10 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = K / S::BK;
   // Prologue: steps 0 .. NS - 1 in flight; stage 0 visible; its first k-substep's fragments read.
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
-    if (s < nk) dma(s, s);
-  wait_steps<S::kDma>(min(nk - 1, NS - 1));
+  for (int s = 0; s < NS; ++s) dma(s, s);
+  wait_vmcnt_imm<(NS - 1) * S::kDma>();
   lds_barrier();
   bf16x8 f0a[S::TM], f0b[S::TN], f1a[S::TM], f1b[S::TN];
 #pragma unroll
@@ -212,6 +206,9 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   // Step kt on stage kt % NS: read k-substep 1 and multiply k-substep 0; wait for this wave's reads and for stage
   // kt + 1's loads, barrier (everyone is then past its reads of stage kt, and stage kt + 1 is visible); refill stage
   // kt % NS with step kt + NS; read the next step's k-substep 0 and multiply k-substep 1.
+  // The reads and loads of each half are spread between its MFMAs (one per MFMA), so that neither the LDS nor the
+  // texture-address queue sees a burst.
+  static_assert(S::TM * S::TN == 16 && S::TM + S::TN == 8 && S::kDma >= 8 && S::kDma <= 10, "interleave patterns");
   for (int kt = 0; kt < nk; ++kt) {
     const int pb = (kt % NS) * kStage;
 #pragma unroll
@@ -223,26 +220,46 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0a[i], f0b[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    wait_steps<S::kDma>(max(0, min(nk - 2 - kt, NS - 2)));
+    wait_vmcnt_imm<(NS - 2) * S::kDma>();  // stage kt + 1 has landed (the loads of kt + 2, kt + 3 may still fly)
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + NS < nk) dma(kt + NS, kt % NS);
-    if (kt + 1 < nk) {
-      const int nb = ((kt + 1) % NS) * kStage;
+    dma(kt + NS, kt % NS);
+    const int nb = ((kt + 1) % NS) * kStage;
 #pragma unroll
-      for (int i = 0; i < S::TM; ++i) f0a[i] = frag(fa_off[0] + nb + i * kTileStride);
+    for (int i = 0; i < S::TM; ++i) f0a[i] = frag(fa_off[0] + nb + i * kTileStride);
 #pragma unroll
-      for (int j = 0; j < S::TN; ++j) f0b[j] = frag(fb_off[0] + nb + j * kTileStride);
-    }
+    for (int j = 0; j < S::TN; ++j) f0b[j] = frag(fb_off[0] + nb + j * kTileStride);
 #pragma unroll
     for (int i = 0; i < S::TM; ++i)
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1a[i], f1b[j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, S::kDma > 8 ? 2 : 1, 0);  // DMA loads (2 after the first MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // when a step has 10)
+    __builtin_amdgcn_sched_group_barrier(0x020, S::kDma > 9 ? 2 : 1, 0);
+#pragma unroll
+    for (int g = 0; g < 6; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __syncthreads();  // every wave is done reading the stages before the epilogue reuses the LDS
+  wait_vmcnt_imm<0>();  // the loads issued past the last step have landed
+  __syncthreads();      // every wave is done with the stages before the epilogue reuses the LDS
 
   // Epilogue through LDS. The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul
   // output, to which it then adds its fp32 rank-1 term -- and staged as the whole tile. Each wave then takes
