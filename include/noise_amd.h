@@ -95,7 +95,8 @@ typedef struct noise_gpt {
   const float* x0_lambdas;    /* fp32 [n_layer] */
   const float* wte;           /* fp32 [padded_vocab, 512] */
   const uint16_t* lm_head;    /* bf16 [padded_vocab, 512] */
-  const float* rope_cos;      /* fp32 [T, 32]: the bf16 rotary table's values (utils/model.py:177-183) */
+  const float* rope_cos;      /* fp32 [T, 32]: the bf16 rotary table's values (utils/model.py:177-183); the kernels
+                                 read them at bf16 precision */
   const float* rope_sin;
   noise_layer layers[NOISE_MAX_LAYERS];
 } noise_gpt;

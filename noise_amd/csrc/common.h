@@ -27,6 +27,13 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t v) { return __uint_as_float(
 // Round-to-nearest-even fp32 -> bf16, the rounding of torch's .to(torch.bfloat16) (gfx950 converts in hardware).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
+// Two floats as a bf16 pair (low half first), and back.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
 // Hardware 2^x and 1/x (v_exp_f32, v_rcp_f32: about 1 ulp, no denormal-range fix-ups), for softmax weights and
 // soft caps whose arguments are bounded.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

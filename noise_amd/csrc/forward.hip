@@ -227,9 +227,11 @@ struct EpiQKV {
     int tok;
     f32x4 a, b_ve;
   };
+  // q / k columns: the row's cos and sin values, packed as bf16 pairs (the rotary tables hold bf16 values, so the
+  // packing is exact); v columns: the row's value-embedding values (fp32 bits) and its gate.
   struct Pre {
-    f32x4 p0[kEpiRows], p1[kEpiRows];  // q / k columns: cos, sin rows; v columns: value-embedding rows (p0)
-    float g[kEpiRows];                 // v columns: gates
+    u32x4 w[kEpiRows];
+    float g[kEpiRows];
   };
   __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
     const int m = mb.member(row_base);
@@ -260,13 +262,14 @@ struct EpiQKV {
       const int j = 4 * (lane & 7);
 #pragma unroll
       for (int q = 0; q < kEpiRows; ++q) {
-        p.p0[q] = ld4(cos_t + (w.t0 + i0 + q) * 32 + j);
-        p.p1[q] = ld4(sin_t + (w.t0 + i0 + q) * 32 + j);
+        const f32x4 c = ld4(cos_t + (w.t0 + i0 + q) * 32 + j), sn = ld4(sin_t + (w.t0 + i0 + q) * 32 + j);
+        p.w[q] = u32x4{pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3]), pack_bf16x2(sn[0], sn[1]),
+                       pack_bf16x2(sn[2], sn[3])};
       }
     } else if (ve) {
 #pragma unroll
       for (int q = 0; q < kEpiRows; ++q) {
-        p.p0[q] = ld4(ve + (int64_t)lane_val(w.tok, i0 + q) * kD + w.c);
+        p.w[q] = __builtin_bit_cast(u32x4, ld4(ve + (int64_t)lane_val(w.tok, i0 + q) * kD + w.c));
         p.g[q] = gate[(int64_t)(row0 + q) * kH + (w.c >> 6)];
       }
     }
@@ -287,11 +290,13 @@ struct EpiQKV {
       const bool first = (lane & 15) < 8;
 #pragma unroll
       for (int q = 0; q < R; ++q) {
+        const float cs[4] = {bf16_lo(p.w[q][0]), bf16_hi(p.w[q][0]), bf16_lo(p.w[q][1]), bf16_hi(p.w[q][1])};
+        const float sn[4] = {bf16_lo(p.w[q][2]), bf16_hi(p.w[q][2]), bf16_lo(p.w[q][3]), bf16_hi(p.w[q][3])};
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float other = __shfl_xor(v[q][e], 8, 64);
-          v[q][e] = first ? v[q][e] * p.p0[q][e] + other * p.p1[q][e] : -other * p.p1[q][e] + v[q][e] * p.p0[q][e];
+          v[q][e] = first ? v[q][e] * cs[e] + other * sn[e] : -other * sn[e] + v[q][e] * cs[e];
           ss += v[q][e] * v[q][e];
         }
 #pragma unroll
@@ -304,8 +309,9 @@ struct EpiQKV {
 #pragma unroll
       for (int q = 0; q < R; ++q) {
         const float at = lane_val(w.at, i0 + q);
+        const f32x4 e4 = __builtin_bit_cast(f32x4, p.w[q]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[q][e] += p.g[q] * (p.p0[q][e] + at * w.b_ve[e]);
+        for (int e = 0; e < 4; ++e) v[q][e] += p.g[q] * (e4[e] + at * w.b_ve[e]);
       }
     }
 #pragma unroll
@@ -604,8 +610,8 @@ __global__ __launch_bounds__(256) void member_sum_kernel(const float* __restrict
   if (threadIdx.x == 0) out[m] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-using Tile = GemmShape<256, 256, 32, 2, 2>;
-using RowTile = GemmShape<128, 512, 32, 1, 4>;  // whole 512-wide rows, for the epilogues that normalize
+using Tile = GemmShape<128, 256, 32, 2, 2, 3, 2>;  // two workgroups per CU: one's epilogue beside the other's MFMAs
+using RowTile = GemmShape<128, 512, 32, 1, 4>;     // whole 512-wide rows, for the epilogues that normalize
 constexpr int kAttnOG = 1;  // 32 outputs per wave (2 waves per SIMD)
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }

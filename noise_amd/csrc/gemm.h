@@ -3,9 +3,11 @@
 // is where the population-specific work (rank-1 member corrections, residual adds, relu^2, soft-capped CE) happens.
 //
 // Tiling: a workgroup computes 256 x 256 with 2 x 2 waves, or 128 x 512 with 1 x 4 waves (whole 512-wide rows, for
-// epilogues that normalize rows); a wave owns 128 x 128 as 4 x 4 MFMA tiles (v_mfma_f32_32x32x16_bf16). K advances in steps of 32 through kStages LDS stages filled by direct-to-LDS buffer
-// loads (buffer_load_dwordx4 ... lds): the loads of step kt + kStages are issued as soon as every wave is done with
-// step kt, so up to three steps of loads are in flight behind the MFMAs and no register holds staged data.
+// epilogues that normalize rows); a wave owns 128 x 128 as 4 x 4 MFMA tiles (v_mfma_f32_32x32x16_bf16). The
+// 128 x 256 tile (waves of 64 x 128) is sized for two workgroups per CU, so that one workgroup's epilogue runs beside
+// the other's MFMAs. K advances in steps of 32 through kStages LDS stages filled by direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds): the loads of step kt + kStages are issued as soon as every wave is done with step
+// kt, so kStages - 1 steps of loads are in flight behind the MFMAs and no register holds staged data.
 // One barrier per step, placed between the step's two 16-deep k-substeps: the second k-substep's fragments are
 // read before it and the next step's first fragments after it, so LDS latency hides behind MFMAs.
 // An LDS row is 32 bf16 = 4 16-byte chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 lanes of a
@@ -23,13 +25,14 @@ namespace noise {
 
 constexpr int kEpiRows = 8;  // rows per epilogue group: consecutive, 8-aligned, so never across a member boundary
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_ = 4, int MINB_ = 1>
 struct GemmShape {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
   static constexpr int kThreads = WM * WN * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
-  static constexpr int kStages = 4;
+  static constexpr int kStages = NS_;                 // LDS stages
+  static constexpr int kMinBlocks = MINB_;            // workgroups per CU the registers and LDS are sized for
   static constexpr int kStageBytes = (BM + BN) * BK * 2;  // A rows then B rows
   static constexpr int kADma = BM / 64, kBDma = BN / 64;  // 1 KB direct-to-LDS loads per wave and step
   static constexpr int kDma = kADma + kBDma;
@@ -38,9 +41,12 @@ struct GemmShape {
   static constexpr int kEpiLds = BM * kEpiLd * 2;         // the whole tile in bf16
   static constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
   static constexpr int kWaveRows = BM / 4;                // epilogue rows per wave
-  static_assert(BK == 32 && WTM == 128 && WTN == 128 && kThreads == 256, "main loop: 4 waves of 128x128, K steps of 32");
-  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 512), "tiles: 256x256 or 128x512");
-  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  static_assert(BK == 32 && WTN == 128 && (WTM == 128 || WTM == 64) && kThreads == 256,
+                "main loop: 4 waves of 128x128 or 64x128, K steps of 32");
+  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 512) || (BM == 128 && BN == 256),
+                "tiles: 256x256, 128x512 or 128x256");
+  static_assert(kStages >= 3 && kStages <= 4, "stages");
+  static_assert(kLdsBytes * kMinBlocks <= 160 * 1024, "LDS");
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -114,12 +120,60 @@ __device__ __forceinline__ void epi_group(const Epi& epi, const bf16_t* st, int 
   EpiRows<H>::template run<kEpiRows>(epi, row0, n0, n_tile, lane, w, p, v);
 }
 
+// Instruction interleaving of the main loop's two halves (sched_group_barrier masks: 0x008 MFMA, 0x020 VMEM read,
+// 0x100 LDS read; the counts must be literal constants). First half: the next k-substep's fragment reads, one after
+// each MFMA. Second half: the step's direct-to-LDS loads after the first MFMAs, then the next step's fragment reads.
+template <class S>
+__device__ __forceinline__ void first_half_schedule() {
+  if constexpr (S::TM == 4) {  // 16 MFMAs, 8 reads
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  } else {  // 8 MFMAs, 6 reads
+#pragma unroll
+    for (int g = 0; g < 6; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+}
+template <class S>
+__device__ __forceinline__ void second_half_schedule() {
+  if constexpr (S::TM == 4) {  // 16 MFMAs, 8 or 10 loads, 8 reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, S::kDma > 8 ? 2 : 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, S::kDma > 9 ? 2 : 1, 0);
+#pragma unroll
+    for (int g = 0; g < 6; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  } else {  // 8 MFMAs, 6 loads, 6 reads
+#pragma unroll
+    for (int g = 0; g < 6; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+}
+
 template <class S, class Epi>
-__global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __restrict__ A, int64_t lda,
+__global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(const bf16_t* __restrict__ A, int64_t lda,
                                                               const bf16_t* __restrict__ B, int64_t ldb, int M, int N,
                                                               int K, Epi epi) {
   constexpr int NS = S::kStages;
-  static_assert(NS == 4, "prologue and waits assume 4 stages");
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int kAStage = S::BM * S::BK * 2;  // A rows, then B rows
   constexpr int kStage = S::kStageBytes;
@@ -136,7 +190,8 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   const int grp_rows = min(kGroup, mt - grp * kGroup);
   const int m_tile = grp * kGroup + in_grp % grp_rows, n_tile = in_grp / grp_rows;
   const int m0 = m_tile * S::BM, n0 = n_tile * S::BN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, so in a scalar register
   const int wm = wave / S::WN, wn = wave % S::WN;
   const int a_rows = min(S::BM, M - m0), b_rows = min(S::BN, N - n0);
 
@@ -208,7 +263,6 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
   // kt % NS with step kt + NS; read the next step's k-substep 0 and multiply k-substep 1.
   // The reads and loads of each half are spread between its MFMAs (one per MFMA), so that neither the LDS nor the
   // texture-address queue sees a burst.
-  static_assert(S::TM * S::TN == 16 && S::TM + S::TN == 8 && S::kDma >= 8 && S::kDma <= 10, "interleave patterns");
   for (int kt = 0; kt < nk; ++kt) {
     const int pb = (kt % NS) * kStage;
 #pragma unroll
@@ -220,12 +274,7 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0a[i], f0b[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    first_half_schedule<S>();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     wait_vmcnt_imm<(NS - 2) * S::kDma>();  // stage kt + 1 has landed (the loads of kt + 2, kt + 3 may still fly)
@@ -242,20 +291,7 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nt_kernel(const bf16_t* __re
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1a[i], f1b[j], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, S::kDma > 8 ? 2 : 1, 0);  // DMA loads (2 after the first MFMAs
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // when a step has 10)
-    __builtin_amdgcn_sched_group_barrier(0x020, S::kDma > 9 ? 2 : 1, 0);
-#pragma unroll
-    for (int g = 0; g < 6; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+    second_half_schedule<S>();
     __builtin_amdgcn_sched_barrier(0);
   }
   wait_vmcnt_imm<0>();  // the loads issued past the last step have landed
