@@ -45,6 +45,22 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
+// Sums of 4 per-lane values over the 64 lanes, by a transposed butterfly (7 shuffles): returns the total of value
+// (2 b5 + b4), b5 b4 = bits 5..4 of the lane id (16 lanes hold each total).
+__device__ __forceinline__ float warp_sum4(const float (&p)[4], int lane) {
+  const bool b5 = lane & 32, b4 = lane & 16;
+  float a[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float keep = b5 ? p[2 + j] : p[j], give = b5 ? p[j] : p[2 + j];
+    a[j] = keep + __shfl_xor(give, 32, 64);
+  }
+  float c = (b4 ? a[1] : a[0]) + __shfl_xor(b4 ? a[0] : a[1], 16, 64);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  return c;
+}
+
 // x as held by lane idx; idx must be the same in every lane (v_readlane_b32).
 __device__ __forceinline__ float lane_val(float x, int idx) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), idx));

@@ -220,6 +220,7 @@ struct EpiQKV {
   int Vp;
   const float* cos_t;  // [T, 32]
   const float* sin_t;
+  static constexpr int kRows = kEpiRows;
   struct Wave {
     int row_base, t0, seg, c;
     const float* nr;
@@ -322,8 +323,10 @@ struct EpiQKV {
 // x += acc + s (sum of the xb partials) a (the residual adds of utils/model.py:118-119); with `mix`, then the next
 // block's lambda mix x = (l_r + s eps_r) x + (l_0 + s eps_0) x0 (eggroll.py:77-79); x is written back, and
 // h = norm(x) in bf16 (utils/model.py:46-47) with the dots h . b_k of the next linear's rank-1 terms. The tile holds
-// whole 512-wide rows (128 x 512 tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3.
+// whole 512-wide rows (512-column tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3. Groups of 4
+// rows: the prefetch of x and x0 rows then fits two workgroups per CU.
 struct EpiResidNorm {
+  static constexpr int kRows = 4;
   Members mb;
   float* x;             // [M, 512] residual stream, read and written
   const float* xbp;     // [M, nxb] partial dots of this linear's input with its b
@@ -346,7 +349,7 @@ struct EpiResidNorm {
     f32x4 a[2], b[3][2];
   };
   struct Pre {
-    f32x4 xv[kEpiRows][2], x0v[kEpiRows][2];
+    f32x4 xv[kRows][2], x0v[kRows][2];
   };
   __device__ __forceinline__ void begin(int row_base, int, int lane, Wave& w) const {
     const int m = mb.member(row_base);
@@ -379,7 +382,7 @@ struct EpiResidNorm {
   }
   __device__ __forceinline__ void load(int row0, int, int lane, const Wave&, Pre& p) const {
 #pragma unroll
-    for (int q = 0; q < kEpiRows; ++q)
+    for (int q = 0; q < kRows; ++q)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         p.xv[q][hh] = ld4(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
@@ -389,7 +392,7 @@ struct EpiResidNorm {
   template <int R>
   __device__ __forceinline__ void rows(int row0, int, int, int lane, const Wave& w, const Pre& p,
                                        f32x4 (&v)[R][2]) const {
-    static_assert(R == 8, "warp_sum8 reduces 8 rows");
+    static_assert(R == 4, "warp_sum4 reduces 4 rows");
     const int i0 = row0 - w.row_base;
     float ss[R];
 #pragma unroll
@@ -411,11 +414,11 @@ struct EpiResidNorm {
         *(f32x4*)(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane) = xn;
       }
     }
-    const float tot = warp_sum8(ss, lane);
+    const float tot = warp_sum4(ss, lane);
     float dk[3][R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      const float inv = rsqrtf(lane_val(tot, 8 * q) * (1.0f / kD) + kNormEps);
+      const float inv = rsqrtf(lane_val(tot, 16 * q) * (1.0f / kD) + kNormEps);
 #pragma unroll
       for (int k = 0; k < 3; ++k) dk[k][q] = 0.f;
 #pragma unroll
@@ -434,8 +437,8 @@ struct EpiResidNorm {
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
         if (k >= ndot) break;
-        const float dt = warp_sum8(dk[k], lane);
-        if ((lane & 7) == 0) xb[(int64_t)(row0 + (lane >> 3)) * 4 + k] = dt;
+        const float dt = warp_sum4(dk[k], lane);
+        if ((lane & 15) == 0) xb[(int64_t)(row0 + (lane >> 4)) * 4 + k] = dt;
       }
     }
   }
@@ -453,6 +456,7 @@ struct EpiReluSq {
   int64_t off_next_b;   // noise offset of the next linear's b (its input is this output)
   float* xb_next;       // [M, n_tiles]
   int n_tiles;
+  static constexpr int kRows = kEpiRows;
   struct Wave {
     int row_base;
     const float* nr;
@@ -521,6 +525,7 @@ struct EpiHeadCE {
   float* tgt_logit;   // [M]
   const int64_t* targets;  // [n_seq, T]
   float* logits;      // [M, vocab] or NULL
+  static constexpr int kRows = kEpiRows;
   struct Wave {
     int row_base, tg;  // tg: the lane's row's target, -1 when it is no column index
     const float* nr;

@@ -23,7 +23,8 @@
 
 namespace noise {
 
-constexpr int kEpiRows = 8;  // rows per epilogue group: consecutive, 8-aligned, so never across a member boundary
+constexpr int kEpiRows = 8;  // rows per epilogue group (most epilogues): consecutive and aligned, so never across a
+                             // member boundary
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_ = 4, int MINB_ = 1>
 struct GemmShape {
@@ -43,9 +44,10 @@ struct GemmShape {
   static constexpr int kWaveRows = BM / 4;                // epilogue rows per wave
   static_assert(BK == 32 && WTN == 128 && (WTM == 128 || WTM == 64) && kThreads == 256,
                 "main loop: 4 waves of 128x128 or 64x128, K steps of 32");
-  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 512) || (BM == 128 && BN == 256),
-                "tiles: 256x256, 128x512 or 128x256");
-  static_assert(kStages >= 3 && kStages <= 4, "stages");
+  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 512) || (BM == 128 && BN == 256) ||
+                    (BM == 64 && BN == 512),
+                "tiles: 256x256, 128x512, 128x256 or 64x512");
+  static_assert(kStages >= 2 && kStages <= 4, "stages");
   static_assert(kLdsBytes * kMinBlocks <= 160 * 1024, "LDS");
 };
 
@@ -108,16 +110,17 @@ struct EpiRows<2> {
 template <int ld, int H, class Epi>
 __device__ __forceinline__ void epi_group(const Epi& epi, const bf16_t* st, int row0, int n0, int n_tile, int lane,
                                           const typename Epi::Wave& w, const typename Epi::Pre& p) {
-  f32x4 v[kEpiRows][H];
+  constexpr int R = Epi::kRows;
+  f32x4 v[R][H];
 #pragma unroll
-  for (int k = 0; k < kEpiRows; ++k)
+  for (int k = 0; k < R; ++k)
 #pragma unroll
     for (int hh = 0; hh < H; ++hh) {
       const u32x2 q = *(const u32x2*)(st + k * ld + hh * 256 + 4 * lane);
       v[k][hh] = f32x4{__uint_as_float(q[0] << 16), __uint_as_float(q[0] & 0xFFFF0000u), __uint_as_float(q[1] << 16),
                        __uint_as_float(q[1] & 0xFFFF0000u)};
     }
-  EpiRows<H>::template run<kEpiRows>(epi, row0, n0, n_tile, lane, w, p, v);
+  EpiRows<H>::template run<R>(epi, row0, n0, n_tile, lane, w, p, v);
 }
 
 // Instruction interleaving of the main loop's two halves (sched_group_barrier masks: 0x008 MFMA, 0x020 VMEM read,
@@ -158,9 +161,16 @@ __device__ __forceinline__ void second_half_schedule() {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-  } else {  // 8 MFMAs, 6 loads, 6 reads
+  } else {  // 8 MFMAs, 6 or 9 loads, 6 reads
+    constexpr int kFirst = S::kDma > 6 ? 2 : 1;  // loads after each of the first three MFMAs
 #pragma unroll
-    for (int g = 0; g < 6; ++g) {
+    for (int g = 0; g < 3; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, kFirst, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -299,7 +309,8 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
 
   // Epilogue through LDS. The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul
   // output, to which it then adds its fp32 rank-1 term -- and staged as the whole tile. Each wave then takes
-  // kWaveRows rows (one member's: M and the member length are multiples of 64) in groups of kEpiRows; lane l holds
+  // kWaveRows rows (one member's: M and the member length are multiples of 64) in groups of Epi::kRows (8, or 4 for
+  // epilogues that prefetch much per row); lane l holds
   // columns 4l .. 4l+3 of each 256-column half. The epilogue functor provides
   //   begin(row_base, n0, lane, Wave&)           loads made once per wave (noise vectors, per-row scalars by lane),
   //   load(row0, n0, lane, const Wave&, Pre&)     the per-row data of one group (issued a group ahead),
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
         st[lr * S::kEpiLd + wn * S::WTN + j * 32 + (lane & 31)] = f32_to_bf16(acc[i][j][r]);
       }
   __syncthreads();
-  constexpr int R = kEpiRows, G = S::kWaveRows / kEpiRows, H = S::BN / 256;
+  constexpr int R = Epi::kRows, G = S::kWaveRows / Epi::kRows, H = S::BN / 256;
   static_assert(G % 2 == 0, "groups are processed in pairs");
   const int row_base = m0 + wave * S::kWaveRows;
   if (row_base >= M) return;

@@ -19,6 +19,7 @@ struct EpiLowrank {
   int64_t ldy;
   float* part;        // [M, n_tiles] or NULL
   int n_tiles;
+  static constexpr int kRows = kEpiRows;
   struct Wave {
     int row_base;
     float k;  // the lane's row's s_m u[row]
