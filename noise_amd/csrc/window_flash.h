@@ -56,22 +56,29 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ int vt_swz(int d, int chunk) { return chunk ^ ((d >> 1) & 15); }  // 8-byte chunks
 
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+// gfx950 transposing LDS read (ds_read_b64_tr_b16), spelled out in the device pass only.
+__device__ __forceinline__ v4s ds_read_tr16(const bf16_t* p) {
+#if __HIP_DEVICE_COMPILE__
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) void*)(void*)p);
+#else
+  (void)p;
+  return v4s{0, 0, 0, 0};
+#endif
+}
+
 template <int MODE>
 struct FlashStage {
   u32x4 y[2];  // two 16-byte vectors of the y tile
-  u32x2 v[4];  // kAttn: 4 inputs x 4 channels, bf16
+  u32x4 v[2];  // kAttn, kCenter: value rows, staged like y
   float lse;
 };
 template <>
 struct FlashStage<kCredit> {
   u32x4 y[2];
   f32x4 v[4];  // kCredit: 4 inputs x 4 channels, fp32
-  float lse;
-};
-template <>
-struct FlashStage<kCenter> {
-  u32x4 y[2];
-  u32x4 v[2];  // kCenter: value rows, staged like y
   float lse;
 };
 
@@ -161,9 +168,9 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
   const int kg = tid >> 4, dg = tid & 15;  // V staging: inputs 4 kg .. 4 kg + 3, channels 4 dg .. 4 dg + 3
 
   // Tile loads through buffer resources over this row's inputs: per-lane offsets are fixed, the tile's first input
-  // goes in the scalar offset. y (and kCenter's values) as 64 rows x 8 16-byte chunks, 2 per thread; kAttn / kCredit
-  // values as 4 inputs x 4 channels per thread.
-  constexpr bool kVRows = (MODE == kCenter);
+  // goes in the scalar offset. y (and the kAttn / kCenter values) as 64 rows x 8 16-byte chunks, 2 per thread;
+  // kCredit values as 4 inputs x 4 channels per thread.
+  constexpr bool kVRows = (MODE == kCenter || MODE == kAttn);
   constexpr int kVElt = (MODE == kCredit) ? 4 : 2;  // bytes per value element
   const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)yg, 0, (int)(((int64_t)(T - 1) * a.y_st + 64) * 2), 0x00020000);
@@ -186,16 +193,12 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
 #pragma unroll
     for (int rep = 0; rep < 2; ++rep)
       st.y[rep] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(y_rsrc, y_vo[rep], i0 * y_step, 0));
-    if constexpr (MODE == kAttn) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        st.v[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(v_rsrc, v_vo[k], i0 * v_step, 0));
-    } else if constexpr (MODE == kCredit) {
+    if constexpr (MODE == kCredit) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
         st.v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_vo[k], i0 * v_step, 0));
       st.lse = (tid < 64) ? lse_in[i0 + tid] : 0.f;
-    } else if constexpr (MODE == kCenter) {
+    } else if constexpr (MODE == kCenter || MODE == kAttn) {
 #pragma unroll
       for (int rep = 0; rep < 2; ++rep)
         st.v[rep] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_vo[rep], i0 * v_step, 0));
@@ -208,17 +211,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
       const int row = v >> 3, chunk = v & 7;
       *(u32x4*)(&ys[s][row * 64 + ((chunk ^ ((row >> 1) & 7)) * 8)]) = st.y[rep];
     }
-    if constexpr (MODE == kAttn) {
-      // 4 inputs x 4 channels -> channel-major 8-byte chunks
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        uint32_t e[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) e[k] = (st.v[k][d >> 1] >> ((d & 1) * 16)) & 0xFFFFu;
-        const int ch = 4 * dg + d;
-        *(u32x2*)(&vt_hi[s][ch * 64 + vt_swz(ch, kg) * 4]) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
-      }
-    } else if constexpr (MODE == kCredit) {
+    if constexpr (MODE == kCredit) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         uint32_t hi[4], lo[4];
@@ -235,7 +228,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
         *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
       }
       if (tid < 64) lse_s[s][tid] = st.lse;
-    } else if constexpr (MODE == kCenter) {
+    } else if constexpr (MODE == kCenter || MODE == kAttn) {
 #pragma unroll
       for (int rep = 0; rep < 2; ++rep) {
         const int v = tid + rep * 256;
@@ -395,9 +388,22 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
               const int d = dt * 32 + col;
-              const u32x2 h0 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c0) * 4]);
-              const u32x2 h1 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c1) * 4]);
-              const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
+              bf16x8 vf;
+              if constexpr (MODE == kAttn) {
+                // V rows [input][channel] in LDS; two transposing reads give this lane channel d at the 8 inputs of
+                // its k slots (ds_read_b64_tr_b16: in each 16-lane group, lane j gets element j % 4 of the 8-byte
+                // pieces read by lanes j / 4 + 4 s, s = 0..3; lane a + 4 s reads channels d0 + 4 a .. of input s)
+                const int grp = lane >> 4;
+                const int d0 = dt * 32 + 16 * (grp & 1) + 4 * (lane & 3);
+                const int i_a = base + 4 * (grp >> 1) + ((lane >> 2) & 3), i_b = i_a + 8;
+                const v4s ra = ds_read_tr16(&vt_hi[s][i_a * 64 + (((d0 >> 3) ^ ((i_a >> 1) & 7)) * 8) + (d0 & 7)]);
+                const v4s rb = ds_read_tr16(&vt_hi[s][i_b * 64 + (((d0 >> 3) ^ ((i_b >> 1) & 7)) * 8) + (d0 & 7)]);
+                vf = __builtin_bit_cast(bf16x8, s16x8{ra[0], ra[1], ra[2], ra[3], rb[0], rb[1], rb[2], rb[3]});
+              } else {
+                const u32x2 h0 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c0) * 4]);
+                const u32x2 h1 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c1) * 4]);
+                vf = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
+              }
 #pragma unroll
               for (int og = 0; og < OG; ++og)
                 if (any[og]) o_acc[og][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[og], o_acc[og][dt], 0, 0, 0);
