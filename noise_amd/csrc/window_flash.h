@@ -14,9 +14,10 @@
 // tile's MFMAs (one barrier per tile). Scores are computed transposed, S^T[i, o] = y_i . x_o (v_mfma_f32_32x32x16_bf16,
 // y from LDS as the A operand, x in registers as the B operand): the accumulator layout of S^T (lane = output l%32,
 // registers = 16 inputs) is exactly the B-operand layout of O^T[d, o] += V^T[d, i] P^T[i, o], so probabilities go
-// from score registers to the value MFMA without an LDS round trip. Every y and V^T fragment read from LDS feeds all
-// output groups of a wave. V^T is written to LDS in 8-byte chunks (4 inputs of one channel) after a 4x4 register
-// transpose; chunks are XOR-swizzled so a half-wave's reads hit distinct banks.
+// from score registers to the value MFMA without an LDS round trip. Every y and V fragment read from LDS feeds all
+// output groups of a wave. Values are staged row-major like y (16-byte chunks XOR-swizzled by row, so a half-wave's
+// reads hit distinct banks; kCredit's fp32 source as bf16 high and low parts), and the V^T operand fragments are
+// read with gfx950's transposing LDS read (ds_read_b64_tr_b16).
 //
 // kCenter computes the value scores the same way as the logits, S2^T[i, o] = v_i . hub_o (v staged in LDS like y,
 // hub in registers like x), and accumulates sum_i p_i s2_i beside sum_i p_i with fp32 probabilities.
@@ -54,7 +55,6 @@ constexpr int kFlashBI = 64;
 template <int OG> struct FlashTile { static constexpr int BO = 4 * 32 * OG; };  // outputs per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ int vt_swz(int d, int chunk) { return chunk ^ ((d >> 1) & 15); }  // 8-byte chunks
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -78,7 +78,7 @@ struct FlashStage {
 template <>
 struct FlashStage<kCredit> {
   u32x4 y[2];
-  f32x4 v[4];  // kCredit: 4 inputs x 4 channels, fp32
+  f32x4 v[4];  // kCredit: 4 16-byte chunks (4 channels) of fp32 value rows
   float lse;
 };
 
@@ -165,11 +165,10 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
   i_begin = i_begin / kFlashBI * kFlashBI;
 
   const float* lse_in = (MODE == kCredit) ? a.lse_in + ((int64_t)b * a.heads + head) * T : nullptr;
-  const int kg = tid >> 4, dg = tid & 15;  // V staging: inputs 4 kg .. 4 kg + 3, channels 4 dg .. 4 dg + 3
 
   // Tile loads through buffer resources over this row's inputs: per-lane offsets are fixed, the tile's first input
   // goes in the scalar offset. y (and the kAttn / kCenter values) as 64 rows x 8 16-byte chunks, 2 per thread;
-  // kCredit values as 4 inputs x 4 channels per thread.
+  // kCredit values (fp32) as 64 rows x 16 16-byte chunks, 4 per thread.
   constexpr bool kVRows = (MODE == kCenter || MODE == kAttn);
   constexpr int kVElt = (MODE == kCredit) ? 4 : 2;  // bytes per value element
   const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -187,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
 #pragma unroll
   for (int k = 0; k < 4; ++k)
     v_vo[k] = kVRows ? (k < 2 ? (((tid + k * 256) >> 3) * (int)a.v_st + ((tid + k * 256) & 7) * 8) * 2 : 0)
-                     : ((4 * kg + k) * (int)a.v_st + 4 * dg) * kVElt;
+                     : (((tid + k * 256) >> 4) * (int)a.v_st + ((tid + k * 256) & 15) * 4) * kVElt;
 
   auto load = [&](int i0, FlashStage<MODE>& st) {
 #pragma unroll
@@ -212,20 +211,21 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
       *(u32x4*)(&ys[s][row * 64 + ((chunk ^ ((row >> 1) & 7)) * 8)]) = st.y[rep];
     }
     if constexpr (MODE == kCredit) {
+      // row-major like the kAttn values: 4 channels of row i as bf16 high and low parts, 8 bytes each
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        uint32_t hi[4], lo[4];
+      for (int k = 0; k < 4; ++k) {
+        const int v = tid + k * 256, row = v >> 4, c4 = v & 15;
+        uint32_t hi[2], lo[2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float f = st.v[k][d];
-          const bf16_t h = f32_to_bf16(f);
-          hi[k] = h;
-          lo[k] = f32_to_bf16(f - bf16_to_f32(h));
+        for (int j = 0; j < 2; ++j) {
+          const float f0 = st.v[k][2 * j], f1 = st.v[k][2 * j + 1];
+          const bf16_t h0 = f32_to_bf16(f0), h1 = f32_to_bf16(f1);
+          hi[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+          lo[j] = pack_bf16x2(f0 - bf16_to_f32(h0), f1 - bf16_to_f32(h1));
         }
-        const int ch = 4 * dg + d;
-        const int at = ch * 64 + vt_swz(ch, kg) * 4;
-        *(u32x2*)(&vt_hi[s][at]) = u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
-        *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+        const int at = row * 64 + (((c4 >> 1) ^ ((row >> 1) & 7)) * 8) + (c4 & 1) * 4;
+        *(u32x2*)(&vt_hi[s][at]) = u32x2{hi[0], hi[1]};
+        *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0], lo[1]};
       }
       if (tid < 64) lse_s[s][tid] = st.lse;
     } else if constexpr (MODE == kCenter || MODE == kAttn) {
@@ -384,33 +384,24 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
 #pragma unroll
               for (int jj = 0; jj < 8; ++jj) pf[og][jj] = (__bf16)sc[og][t][sp * 8 + jj];
             const int base = t * 32 + sp * 16;
-            const int c0 = (base + 4 * half) >> 2, c1 = (base + 8 + 4 * half) >> 2;
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
-              const int d = dt * 32 + col;
-              bf16x8 vf;
-              if constexpr (MODE == kAttn) {
-                // V rows [input][channel] in LDS; two transposing reads give this lane channel d at the 8 inputs of
-                // its k slots (ds_read_b64_tr_b16: in each 16-lane group, lane j gets element j % 4 of the 8-byte
-                // pieces read by lanes j / 4 + 4 s, s = 0..3; lane a + 4 s reads channels d0 + 4 a .. of input s)
-                const int grp = lane >> 4;
-                const int d0 = dt * 32 + 16 * (grp & 1) + 4 * (lane & 3);
-                const int i_a = base + 4 * (grp >> 1) + ((lane >> 2) & 3), i_b = i_a + 8;
-                const v4s ra = ds_read_tr16(&vt_hi[s][i_a * 64 + (((d0 >> 3) ^ ((i_a >> 1) & 7)) * 8) + (d0 & 7)]);
-                const v4s rb = ds_read_tr16(&vt_hi[s][i_b * 64 + (((d0 >> 3) ^ ((i_b >> 1) & 7)) * 8) + (d0 & 7)]);
-                vf = __builtin_bit_cast(bf16x8, s16x8{ra[0], ra[1], ra[2], ra[3], rb[0], rb[1], rb[2], rb[3]});
-              } else {
-                const u32x2 h0 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c0) * 4]);
-                const u32x2 h1 = *(const u32x2*)(&vt_hi[s][d * 64 + vt_swz(d, c1) * 4]);
-                vf = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
-              }
+              // Values are rows [input][channel] in LDS; two transposing reads give this lane channel d at the 8 inputs
+              // of its k slots (ds_read_b64_tr_b16: in each 16-lane group, lane j gets element j % 4 of the 8-byte
+              // pieces read by lanes j / 4 + 4 s, s = 0..3; lane a + 4 s reads channels d0 + 4 a .. of input s).
+              const int grp = lane >> 4;
+              const int d0 = dt * 32 + 16 * (grp & 1) + 4 * (lane & 3);
+              const int i_a = base + 4 * (grp >> 1) + ((lane >> 2) & 3), i_b = i_a + 8;
+              const int at_a = i_a * 64 + (((d0 >> 3) ^ ((i_a >> 1) & 7)) * 8) + (d0 & 7);
+              const int at_b = i_b * 64 + (((d0 >> 3) ^ ((i_b >> 1) & 7)) * 8) + (d0 & 7);
+              const v4s ra = ds_read_tr16(&vt_hi[s][at_a]), rb = ds_read_tr16(&vt_hi[s][at_b]);
+              const bf16x8 vf = __builtin_bit_cast(bf16x8, s16x8{ra[0], ra[1], ra[2], ra[3], rb[0], rb[1], rb[2], rb[3]});
 #pragma unroll
               for (int og = 0; og < OG; ++og)
                 if (any[og]) o_acc[og][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[og], o_acc[og][dt], 0, 0, 0);
               if (MODE == kCredit && a.hi_lo) {
-                const u32x2 g0 = *(const u32x2*)(&vt_lo[s][d * 64 + vt_swz(d, c0) * 4]);
-                const u32x2 g1 = *(const u32x2*)(&vt_lo[s][d * 64 + vt_swz(d, c1) * 4]);
-                const bf16x8 lf = __builtin_bit_cast(bf16x8, u32x4{g0[0], g0[1], g1[0], g1[1]});
+                const v4s ga = ds_read_tr16(&vt_lo[s][at_a]), gb = ds_read_tr16(&vt_lo[s][at_b]);
+                const bf16x8 lf = __builtin_bit_cast(bf16x8, s16x8{ga[0], ga[1], ga[2], ga[3], gb[0], gb[1], gb[2], gb[3]});
 #pragma unroll
                 for (int og = 0; og < OG; ++og)
                   if (any[og]) o_acc[og][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lf, pf[og], o_acc[og][dt], 0, 0, 0);
