@@ -34,6 +34,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
 
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+// gfx950 transposing LDS read (ds_read_b64_tr_b16), spelled out in the device pass only.
+__device__ __forceinline__ v4s ds_read_tr16(const bf16_t* p) {
+#if __HIP_DEVICE_COMPILE__
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) void*)(void*)p);
+#else
+  (void)p;
+  return v4s{0, 0, 0, 0};
+#endif
+}
+
 // Hardware 2^x and 1/x (v_exp_f32, v_rcp_f32: about 1 ulp, no denormal-range fix-ups), for softmax weights and
 // soft caps whose arguments are bounded.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -56,19 +56,6 @@ template <int OG> struct FlashTile { static constexpr int BO = 4 * 32 * OG; };  
 constexpr float kLog2e = 1.4426950408889634f;
 
 
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-// gfx950 transposing LDS read (ds_read_b64_tr_b16), spelled out in the device pass only.
-__device__ __forceinline__ v4s ds_read_tr16(const bf16_t* p) {
-#if __HIP_DEVICE_COMPILE__
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) void*)(void*)p);
-#else
-  (void)p;
-  return v4s{0, 0, 0, 0};
-#endif
-}
-
 template <int MODE>
 struct FlashStage {
   u32x4 y[2];  // two 16-byte vectors of the y tile
