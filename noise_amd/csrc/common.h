@@ -58,20 +58,52 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
-// Sums of 4 per-lane values over the 64 lanes, by a transposed butterfly (7 shuffles): returns the total of value
-// (2 b5 + b4), b5 b4 = bits 5..4 of the lane id (16 lanes hold each total).
-__device__ __forceinline__ float warp_sum4(const float (&p)[4], int lane) {
-  const bool b5 = lane & 32, b4 = lane & 16;
-  float a[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const float keep = b5 ? p[2 + j] : p[j], give = b5 ? p[j] : p[2 + j];
-    a[j] = keep + __shfl_xor(give, 32, 64);
-  }
-  float c = (b4 ? a[1] : a[0]) + __shfl_xor(b4 ? a[0] : a[1], 16, 64);
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+// Cross-lane moves without the LDS crossbar. dpp_mov<CTRL>: a DPP row control (0xB1 quad_perm [1,0,3,2], 0x4E
+// quad_perm [2,3,0,1], 0x141 row_half_mirror, 0x140 row_mirror, 0x128 row_ror:8). lane_swap32(a, b): a takes
+// {a[0:31], b[0:31]} and b takes {a[32:63], b[32:63]} (v_permlane32_swap). lane_swap16(a, b): rows of 16 lanes,
+// a takes {a.r0, b.r0, a.r2, b.r2} and b takes {a.r1, b.r1, a.r3, b.r3} (v_permlane16_swap). The builtins are
+// spelled out in the device pass only.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+#if __HIP_DEVICE_COMPILE__
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+#else
+  return x;
+#endif
+}
+__device__ __forceinline__ void lane_swap32(float& a, float& b) {
+#if __HIP_DEVICE_COMPILE__
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+#endif
+}
+__device__ __forceinline__ void lane_swap16(float& a, float& b) {
+#if __HIP_DEVICE_COMPILE__
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+#endif
+}
+// Sum over each 8-lane group, in every lane of the group (each step adds a lane's partner, so all lanes agree).
+__device__ __forceinline__ float group_sum8(float c) {
+  c += dpp_mov<0xB1>(c);
+  c += dpp_mov<0x4E>(c);
+  c += dpp_mov<0x141>(c);
   return c;
+}
+
+// Sums of 4 per-lane values over the 64 lanes, by a transposed butterfly (halves swapped, then rows, then within a
+// row): returns the total of value (2 b5 + b4), b5 b4 = bits 5..4 of the lane id (the 16 lanes of row q hold the
+// total of value q).
+__device__ __forceinline__ float warp_sum4(const float (&p)[4], int) {
+  float a0 = p[0], b0 = p[2], a1 = p[1], b1 = p[3];
+  lane_swap32(a0, b0);
+  lane_swap32(a1, b1);
+  float s0 = a0 + b0, s1 = a1 + b1;  // lanes 0..31: values 0, 1; lanes 32..63: values 2, 3
+  lane_swap16(s0, s1);
+  const float c = group_sum8(s0 + s1);
+  return c + dpp_mov<0x140>(c);
 }
 
 // x as held by lane idx; idx must be the same in every lane (v_readlane_b32).
@@ -80,27 +112,27 @@ __device__ __forceinline__ float lane_val(float x, int idx) {
 }
 __device__ __forceinline__ int lane_val(int x, int idx) { return __builtin_amdgcn_readlane(x, idx); }
 
-// Sums of 8 per-lane values over the 64 lanes, by a transposed butterfly (10 shuffles instead of 8 x 6): returns
-// the total of value (4 b5 + 2 b4 + b3) where b5 b4 b3 are bits 5..3 of the lane id (8 lanes hold each total).
+// Sums of 8 per-lane values over the 64 lanes, by a transposed butterfly (halves, rows, half-rows, then within 8
+// lanes): returns the total of value (4 b5 + 2 b4 + b3) where b5 b4 b3 are bits 5..3 of the lane id (8 lanes hold
+// each total).
 __device__ __forceinline__ float warp_sum8(const float (&p)[8], int lane) {
-  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
   float q[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const float send = b5 ? p[r] : p[r + 4];
-    q[r] = (b5 ? p[r + 4] : p[r]) + __shfl_xor(send, 32, 64);
+    float a = p[r], b = p[r + 4];
+    lane_swap32(a, b);
+    q[r] = a + b;  // lanes 0..31: value r; lanes 32..63: value r + 4
   }
   float w[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const float send = b4 ? q[r] : q[r + 2];
-    w[r] = (b4 ? q[r + 2] : q[r]) + __shfl_xor(send, 16, 64);
+    float a = q[r], b = q[r + 2];
+    lane_swap16(a, b);
+    w[r] = a + b;  // rows 0..3: values r, r + 2, r + 4, r + 6
   }
-  float z = (b3 ? w[1] : w[0]) + __shfl_xor(b3 ? w[0] : w[1], 8, 64);
-  z += __shfl_xor(z, 4, 64);
-  z += __shfl_xor(z, 2, 64);
-  z += __shfl_xor(z, 1, 64);
-  return z;
+  const bool b3 = lane & 8;
+  const float z = (b3 ? w[1] : w[0]) + dpp_mov<0x128>(b3 ? w[0] : w[1]);
+  return group_sum8(z);
 }
 
 __device__ __forceinline__ float warp_max(float v) {

@@ -234,7 +234,7 @@ struct EpiQKV {
     u32x4 w[kEpiRows];
     float g[kEpiRows];
   };
-  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, int nrows, Wave& w) const {
     const int m = mb.member(row_base);
     w.row_base = row_base;
     w.t0 = row_base - m * mb.T;
@@ -246,10 +246,10 @@ struct EpiQKV {
     w.a = w.b_ve = f32x4{0.f, 0.f, 0.f, 0.f};
     if (w.nr) {
       w.a = ld4(w.nr + off[w.seg] + w.c);
-      w.xb = xb[(int64_t)(row_base + lane) * 4 + w.seg];
+      if (lane < nrows) w.xb = xb[(int64_t)(row_base + lane) * 4 + w.seg];
     }
     if (w.seg == 2 && ve) {
-      const int64_t tk = mb.tokens[(int64_t)mb.seq[m] * mb.T + w.t0 + lane];
+      const int64_t tk = lane < nrows ? mb.tokens[(int64_t)mb.seq[m] * mb.T + w.t0 + lane] : 0;
       w.tok = (tk < 0 || tk >= Vp) ? 0 : (int)tk;
       if (w.nr) {
         w.at = w.s * w.nr[off_ve + w.tok];
@@ -320,11 +320,13 @@ struct EpiQKV {
   }
 };
 
-// x += acc + s (sum of the xb partials) a (the residual adds of utils/model.py:118-119); with `mix`, then the next
+// x += acc + s (sum of the xb partials) a (the residual adds of utils/model.py:118-119); with kMix, then the next
 // block's lambda mix x = (l_r + s eps_r) x + (l_0 + s eps_0) x0 (eggroll.py:77-79); x is written back, and
-// h = norm(x) in bf16 (utils/model.py:46-47) with the dots h . b_k of the next linear's rank-1 terms. The tile holds
-// whole 512-wide rows (512-column tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3. Groups of 4
-// rows: the prefetch of x and x0 rows then fits two workgroups per CU.
+// h = norm(x) in bf16 (utils/model.py:46-47) with the kNDot dots h . b_k of the next linear's rank-1 terms. The tile
+// holds whole 512-wide rows (512-column tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3. Groups of
+// 4 rows keep the x and x0 prefetch small. The rank-1 term is added unconditionally: its a and dot are zero for rows
+// without noise.
+template <bool kMix, int kNDot>
 struct EpiResidNorm {
   static constexpr int kRows = 4;
   Members mb;
@@ -332,26 +334,24 @@ struct EpiResidNorm {
   const float* xbp;     // [M, nxb] partial dots of this linear's input with its b
   int nxb;
   int64_t off;          // noise offset of this linear's a
-  int mix;
   const float* x0;      // [M, 512] (mix only)
   const float* resid_lambdas;
   const float* x0_lambdas;
   int layer;            // the block whose lambdas mix
   int64_t off_resid, off_x0;
   bf16_t* h;            // [M, 512]
-  int ndot;
-  int64_t off_b[3];     // noise offsets of the next linear's b vectors
+  int64_t off_b[3];     // noise offsets of the next linear's b vectors (kNDot of them)
   float* xb;            // [M, 4]
   struct Wave {
     int row_base;
     const float* nr;
     float s, d, lr, l0;
-    f32x4 a[2], b[3][2];
+    f32x4 a[2], b[kNDot][2];
   };
   struct Pre {
     f32x4 xv[kRows][2], x0v[kRows][2];
   };
-  __device__ __forceinline__ void begin(int row_base, int, int lane, Wave& w) const {
+  __device__ __forceinline__ void begin(int row_base, int, int lane, int nrows, Wave& w) const {
     const int m = mb.member(row_base);
     w.row_base = row_base;
     w.nr = mb.nrow(m);
@@ -361,20 +361,20 @@ struct EpiResidNorm {
     for (int hh = 0; hh < 2; ++hh) {
       w.a[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < 3; ++k) w.b[k][hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < kNDot; ++k) w.b[k][hh] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     if (w.nr) {
-      for (int p = 0; p < nxb; ++p) w.d += xbp[(int64_t)(row_base + lane) * nxb + p];
+      if (lane < nrows)
+        for (int p = 0; p < nxb; ++p) w.d += xbp[(int64_t)(row_base + lane) * nxb + p];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         w.a[hh] = ld4(w.nr + off + hh * 256 + 4 * lane);
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
-          if (k < ndot) w.b[k][hh] = ld4(w.nr + off_b[k] + hh * 256 + 4 * lane);
+        for (int k = 0; k < kNDot; ++k) w.b[k][hh] = ld4(w.nr + off_b[k] + hh * 256 + 4 * lane);
       }
     }
     w.lr = 1.f; w.l0 = 0.f;
-    if (mix) {
+    if (kMix) {
       w.lr = resid_lambdas[layer];
       w.l0 = x0_lambdas[layer];
       if (w.nr) { w.lr += w.s * w.nr[off_resid + layer]; w.l0 += w.s * w.nr[off_x0 + layer]; }
@@ -386,7 +386,7 @@ struct EpiResidNorm {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         p.xv[q][hh] = ld4(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
-        if (mix) p.x0v[q][hh] = ld4(x0 + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
+        if (kMix) p.x0v[q][hh] = ld4(x0 + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
       }
   }
   template <int R>
@@ -397,7 +397,7 @@ struct EpiResidNorm {
     float ss[R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      const float d = w.nr ? lane_val(w.d, i0 + q) : 0.f;
+      const float d = lane_val(w.d, i0 + q);
       ss[q] = 0.f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -405,9 +405,9 @@ struct EpiResidNorm {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float val = v[q][hh][e];
-          if (w.nr) val += w.s * d * w.a[hh][e];
+          val += w.s * d * w.a[hh][e];
           xn[e] += val;
-          if (mix) xn[e] = w.lr * xn[e] + w.l0 * p.x0v[q][hh][e];
+          if (kMix) xn[e] = w.lr * xn[e] + w.l0 * p.x0v[q][hh][e];
           ss[q] += xn[e] * xn[e];
         }
         v[q][hh] = xn;
@@ -415,12 +415,12 @@ struct EpiResidNorm {
       }
     }
     const float tot = warp_sum4(ss, lane);
-    float dk[3][R];
+    float dk[kNDot][R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
       const float inv = rsqrtf(lane_val(tot, 16 * q) * (1.0f / kD) + kNormEps);
 #pragma unroll
-      for (int k = 0; k < 3; ++k) dk[k][q] = 0.f;
+      for (int k = 0; k < kNDot; ++k) dk[k][q] = 0.f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         f32x4 hv;
@@ -428,15 +428,14 @@ struct EpiResidNorm {
         for (int e = 0; e < 4; ++e) hv[e] = bf16_to_f32(f32_to_bf16(v[q][hh][e] * inv));
         st_bf16x4(h + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane, hv);
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
+        for (int k = 0; k < kNDot; ++k)
 #pragma unroll
           for (int e = 0; e < 4; ++e) dk[k][q] += hv[e] * w.b[k][hh][e];
       }
     }
     if (w.nr) {
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        if (k >= ndot) break;
+      for (int k = 0; k < kNDot; ++k) {
         const float dt = warp_sum4(dk[k], lane);
         if ((lane & 15) == 0) xb[(int64_t)(row0 + (lane >> 4)) * 4 + k] = dt;
       }
@@ -464,7 +463,7 @@ struct EpiReluSq {
     f32x4 a, b;
   };
   struct Pre {};
-  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, int nrows, Wave& w) const {
     const int m = mb.member(row_base);
     w.row_base = row_base;
     w.nr = mb.nrow(m);
@@ -474,7 +473,7 @@ struct EpiReluSq {
       w.s = mb.sgn(m);
       w.a = ld4(w.nr + off + n0 + 4 * lane);
       w.b = ld4(w.nr + off_next_b + n0 + 4 * lane);
-      w.xb = xb[(int64_t)(row_base + lane) * xb_ld];
+      if (lane < nrows) w.xb = xb[(int64_t)(row_base + lane) * xb_ld];
     }
   }
   __device__ __forceinline__ void load(int, int, int, const Wave&, Pre&) const {}
@@ -533,10 +532,10 @@ struct EpiHeadCE {
     f32x4 a;
   };
   struct Pre {};
-  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, int nrows, Wave& w) const {
     const int m = mb.member(row_base);
     w.row_base = row_base;
-    const int64_t t = targets[(int64_t)mb.seq[m] * mb.T + (row_base - m * mb.T) + lane];
+    const int64_t t = lane < nrows ? targets[(int64_t)mb.seq[m] * mb.T + (row_base - m * mb.T) + lane] : -1;
     w.tg = (t >= 0 && t < vocab) ? (int)t : -1;
     w.nr = mb.nrow(m);
     w.s = 0.f; w.xb = 0.f;
@@ -544,7 +543,7 @@ struct EpiHeadCE {
     if (w.nr) {
       w.s = mb.sgn(m);
       w.a = ld4(w.nr + off + n0 + 4 * lane);
-      w.xb = xb[(int64_t)(row_base + lane) * xb_ld];
+      if (lane < nrows) w.xb = xb[(int64_t)(row_base + lane) * xb_ld];
     }
   }
   __device__ __forceinline__ void load(int, int, int, const Wave&, Pre&) const {}
@@ -656,7 +655,8 @@ static bool g_prepared = false;
 static int prepare_all() {
   if (g_prepared) return NOISE_OK;
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiQKV>()));
-  NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm>()));
+  NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<false, 1>>()));
+  NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3>>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiReluSq>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiHeadCE>()));
   g_prepared = true;
@@ -758,10 +758,10 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     }
 
     // attention projection + residual, then the MLP's norm and c_fc's rank-1 dot
-    EpiResidNorm ep;
+    EpiResidNorm<false, 1> ep;
     memset(&ep, 0, sizeof(ep));
     ep.mb = mb; ep.x = ws.x; ep.xbp = ws.xbp; ep.nxb = kH; ep.off = pert->c_proj[i];
-    ep.h = ws.h; ep.ndot = 1; ep.off_b[0] = pert->c_fc[i] + kF;  // c_fc's a spans its 2048 outputs
+    ep.h = ws.h; ep.off_b[0] = pert->c_fc[i] + kF;  // c_fc's a spans its 2048 outputs
     ep.xb = ws.xb;
     {
       NoiseTimer tm(kTimeProj, stream);
@@ -777,19 +777,21 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     // MLP projection + residual, then the next block's lambda mix, norm and q/k/v dots (or the final norm and
     // lm_head's rank-1 dot)
     const bool last = i + 1 == model->n_layer;
-    EpiResidNorm em;
-    memset(&em, 0, sizeof(em));
-    em.mb = mb; em.x = ws.x; em.xbp = ws.xb1; em.nxb = kF / Tile::BN; em.off = pert->mlp_proj[i];
-    em.h = ws.h; em.xb = ws.xb;
     if (last) {
-      em.ndot = 1; em.off_b[0] = pert->lm_head + Vp;
+      EpiResidNorm<false, 1> em;
+      memset(&em, 0, sizeof(em));
+      em.mb = mb; em.x = ws.x; em.xbp = ws.xb1; em.nxb = kF / Tile::BN; em.off = pert->mlp_proj[i];
+      em.h = ws.h; em.xb = ws.xb; em.off_b[0] = pert->lm_head + Vp;
+      NoiseTimer tm(kTimeMlpProj, stream);
+      NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
     } else {
-      em.mix = 1; em.x0 = ws.x0; em.resid_lambdas = model->resid_lambdas; em.x0_lambdas = model->x0_lambdas;
+      EpiResidNorm<true, 3> em;
+      memset(&em, 0, sizeof(em));
+      em.mb = mb; em.x = ws.x; em.xbp = ws.xb1; em.nxb = kF / Tile::BN; em.off = pert->mlp_proj[i];
+      em.h = ws.h; em.xb = ws.xb;
+      em.x0 = ws.x0; em.resid_lambdas = model->resid_lambdas; em.x0_lambdas = model->x0_lambdas;
       em.layer = i + 1; em.off_resid = pert->resid_lambdas; em.off_x0 = pert->x0_lambdas;
-      em.ndot = 3;
       em.off_b[0] = pert->c_q[i + 1] + kD; em.off_b[1] = pert->c_k[i + 1] + kD; em.off_b[2] = pert->c_v[i + 1] + kD;
-    }
-    {
       NoiseTimer tm(kTimeMlpProj, stream);
       NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
     }

@@ -29,21 +29,24 @@ constexpr int kEpiRows = 8;  // rows per epilogue group (most epilogues): consec
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_ = 4, int MINB_ = 1>
 struct GemmShape {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
-  static constexpr int kThreads = WM * WN * 64;
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = kWaves * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
   static constexpr int kStages = NS_;                 // LDS stages
   static constexpr int kMinBlocks = MINB_;            // workgroups per CU the registers and LDS are sized for
   static constexpr int kStageBytes = (BM + BN) * BK * 2;  // A rows then B rows
-  static constexpr int kADma = BM / 64, kBDma = BN / 64;  // 1 KB direct-to-LDS loads per wave and step
+  static constexpr int kADma = BM / 16 / kWaves, kBDma = BN / 16 / kWaves;  // 1 KB direct-to-LDS loads per wave
+                                                                          // and step
   static constexpr int kDma = kADma + kBDma;
   static constexpr int kEpiLd = BN + 16;                  // bf16 staging row stride (16 elements of padding)
   static constexpr int kMainLds = kStages * kStageBytes;
   static constexpr int kEpiLds = BM * kEpiLd * 2;         // the whole tile in bf16
   static constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
-  static constexpr int kWaveRows = BM / 4;                // epilogue rows per wave
-  static_assert(BK == 32 && WTN == 128 && (WTM == 128 || WTM == 64) && kThreads == 256,
-                "main loop: 4 waves of 128x128 or 64x128, K steps of 32");
+  static constexpr int kWaveRows = BM / kWaves;           // epilogue rows per wave
+  static_assert(BK == 32 && WTN == 128 && (WTM == 128 || WTM == 64) && (kWaves == 4 || kWaves == 8),
+                "main loop: 4 or 8 waves of 128x128 or 64x128, K steps of 32");
+  static_assert(kADma * kWaves * 16 == BM && kBDma * kWaves * 16 == BN, "row groups of 16 split evenly over waves");
   static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 512) || (BM == 128 && BN == 256) ||
                     (BM == 64 && BN == 512),
                 "tiles: 256x256, 128x512, 128x256 or 64x512");
@@ -161,6 +164,16 @@ __device__ __forceinline__ void second_half_schedule() {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+  } else if constexpr (S::kDma == 5) {  // 8 MFMAs, 5 loads, 6 reads
+#pragma unroll
+    for (int g = 0; g < 5; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   } else {  // 8 MFMAs, 6 or 9 loads, 6 reads
     constexpr int kFirst = S::kDma > 6 ? 2 : 1;  // loads after each of the first three MFMAs
 #pragma unroll
@@ -312,7 +325,8 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   // kWaveRows rows (one member's: M and the member length are multiples of 64) in groups of Epi::kRows (8, or 4 for
   // epilogues that prefetch much per row); lane l holds
   // columns 4l .. 4l+3 of each 256-column half. The epilogue functor provides
-  //   begin(row_base, n0, lane, Wave&)           loads made once per wave (noise vectors, per-row scalars by lane),
+  //   begin(row_base, n0, lane, nrows, Wave&)    loads made once per wave (noise vectors, per-row scalars by lane for
+  //                                              the wave's nrows rows),
   //   load(row0, n0, lane, const Wave&, Pre&)     the per-row data of one group (issued a group ahead),
   //   rows<R>(row0, n0, n_tile, lane, const Wave&, const Pre&, v)  the group's arithmetic and stores, with
   //   v = f32x4[R] (256-column tiles) or f32x4[R][2] (512-column tiles: columns 4l.. and 256 + 4l..).
@@ -332,7 +346,7 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   const int row_base = m0 + wave * S::kWaveRows;
   if (row_base >= M) return;
   typename Epi::Wave w;
-  epi.begin(row_base, n0, lane, w);
+  epi.begin(row_base, n0, lane, min(S::kWaveRows, M - row_base), w);  // per-row loads by lane: lanes < nrows
   typename Epi::Pre p0, p1;
   epi.load(row_base, n0, lane, w, p0);
   const bf16_t* st_wave = st + wave * S::kWaveRows * S::kEpiLd;

@@ -26,11 +26,11 @@ struct EpiLowrank {
     f32x4 a;
   };
   struct Pre {};
-  __device__ __forceinline__ void begin(int row_base, int n0, int lane, Wave& w) const {
+  __device__ __forceinline__ void begin(int row_base, int n0, int lane, int nrows, Wave& w) const {
     const int m = row_base / T;
     w.row_base = row_base;
     w.a = *(const f32x4*)(noise + (int64_t)m * stride + a_off + n0 + 4 * lane);
-    w.k = sign[m] * u[row_base + lane];
+    w.k = lane < nrows ? sign[m] * u[row_base + lane] : 0.f;
   }
   __device__ __forceinline__ void load(int, int, int, const Wave&, Pre&) const {}
   template <int R>
