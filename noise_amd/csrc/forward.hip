@@ -141,11 +141,11 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
     }
 #pragma unroll
     for (int hd = 0; hd < kH; ++hd) {
-      g[hd] += __shfl_xor(g[hd], 1, 64);
-      g[hd] += __shfl_xor(g[hd], 2, 64);
+      g[hd] += dpp_mov<0xB1>(g[hd]);  // lane ^ 1
+      g[hd] += dpp_mov<0x4E>(g[hd]);  // lane ^ 2
     }
-    db += __shfl_xor(db, 1, 64);
-    db += __shfl_xor(db, 2, 64);
+    db += dpp_mov<0xB1>(db);
+    db += dpp_mov<0x4E>(db);
     if (lane == 0) {
 #pragma unroll
       for (int hd = 0; hd < kH; ++hd) {
@@ -296,12 +296,12 @@ struct EpiQKV {
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float other = __shfl_xor(v[q][e], 8, 64);
+          const float other = dpp_mov<0x128>(v[q][e]);  // lane ^ 8: the rotary partner in the head's 16 lanes
           v[q][e] = first ? v[q][e] * cs[e] + other * sn[e] : -other * sn[e] + v[q][e] * cs[e];
           ss += v[q][e] * v[q][e];
         }
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        ss = group_sum8(ss);
+        ss += dpp_mov<0x140>(ss);  // the head's 16 lanes
         const float inv = rsqrtf(ss * (1.0f / kHD) + kNormEps);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[q][e] *= inv;
