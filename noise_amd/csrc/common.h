@@ -52,11 +52,6 @@ __device__ __forceinline__ v4s ds_read_tr16(const bf16_t* p) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-__device__ __forceinline__ float warp_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 
 // Cross-lane moves without the LDS crossbar. dpp_mov<CTRL>: a DPP row control (0xB1 quad_perm [1,0,3,2], 0x4E
 // quad_perm [2,3,0,1], 0x141 row_half_mirror, 0x140 row_mirror, 0x128 row_ror:8). lane_swap32(a, b): a takes
@@ -84,6 +79,12 @@ __device__ __forceinline__ void lane_swap16(float& a, float& b) {
   a = __uint_as_float(r[0]);
   b = __uint_as_float(r[1]);
 #endif
+}
+// x of lane l ^ 32.
+__device__ __forceinline__ float lane_xor32(float x, int lane) {
+  float a = x, b = x;
+  lane_swap32(a, b);  // a: {x[0:31], x[0:31]}, b: {x[32:63], x[32:63]}
+  return (lane & 32) ? a : b;
 }
 // Sum over each 8-lane group, in every lane of the group (each step adds a lane's partner, so all lanes agree).
 __device__ __forceinline__ float group_sum8(float c) {
@@ -135,10 +136,39 @@ __device__ __forceinline__ float warp_sum8(const float (&p)[8], int lane) {
   return group_sum8(z);
 }
 
+// Sum / max over the 64 lanes, in every lane (halves, rows, then within a row; each step combines a lane with its
+// partner, so all lanes agree).
+__device__ __forceinline__ float warp_sum(float v) {
+  const int lane = __lane_id();
+  {
+    float a = v, b = v;
+    lane_swap32(a, b);
+    v += (lane & 32) ? a : b;
+  }
+  {
+    float a = v, b = v;
+    lane_swap16(a, b);  // a: {r0, r0, r2, r2}, b: {r1, r1, r3, r3}
+    v += (lane & 16) ? a : b;
+  }
+  v = group_sum8(v);
+  return v + dpp_mov<0x140>(v);
+}
 __device__ __forceinline__ float warp_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  const int lane = __lane_id();
+  {
+    float a = v, b = v;
+    lane_swap32(a, b);
+    v = fmaxf(v, (lane & 32) ? a : b);
+  }
+  {
+    float a = v, b = v;
+    lane_swap16(a, b);
+    v = fmaxf(v, (lane & 16) ? a : b);
+  }
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  return fmaxf(v, dpp_mov<0x140>(v));
 }
 
 // Error state of the C ABI (abi.cpp).

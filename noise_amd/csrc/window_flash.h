@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
               sc[og][t][r] = e;
               mt = fmaxf(mt, e);
             }
-          mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+          mt = fmaxf(mt, lane_xor32(mt, lane));
           const float m_new = fmaxf(m_run[og], mt);
           const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
           const float corr = fast_exp2(m_run[og] - m_safe);
@@ -408,12 +408,12 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
   for (int og = 0; og < OG; ++og) {
     const int my_o = ow + og * 32 + col;
     if (MODE == kAttn || MODE == kLse || MODE == kCenter) {
-      const float l_tot = l_run[og] + __shfl_xor(l_run[og], 32, 64);
+      const float l_tot = l_run[og] + lane_xor32(l_run[og], lane);
       const float mref = bounded ? ref : m_run[og];
       const float lse = (mref + log2f(l_tot)) * (1.0f / kLog2e);
       if (a.lse_out && half == 0) a.lse_out[((int64_t)b * a.heads + head) * T + my_o] = lse;
       if constexpr (MODE == kCenter) {
-        const float c_tot = c_run[og] + __shfl_xor(c_run[og], 32, 64);
+        const float c_tot = c_run[og] + lane_xor32(c_run[og], lane);
         if (half == 0) a.center_out[((int64_t)b * a.heads + head) * T + my_o] = c_tot / l_tot;
       }
       if (MODE == kAttn) {
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
             *(u32x2*)(og_ptr + d) = u32x2{(uint32_t)e[0] | ((uint32_t)e[1] << 16), (uint32_t)e[2] | ((uint32_t)e[3] << 16)};
           }
         if (a.xb_out) {
-          dot += __shfl_xor(dot, 32, 64);
+          dot += lane_xor32(dot, lane);
           if (half == 0) a.xb_out[(b * T + my_o) * a.heads + head] = dot;
         }
       }
