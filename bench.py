@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the population hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload c4|c5] [--no-cpu-baseline] [--no-credit]
+    python bench.py [--steps K] [--warmup W] [--workload c4|c5] [--no-cpu-baseline] [--no-credit] [--no-dust]
     python bench.py --copy-calibration      # one plain 1 GiB device copy, to scale rocprofv3 FETCH/WRITE_SIZE
 
 A step is one pass of the hot path over one batch of synthetic input:
@@ -11,8 +11,8 @@ A step is one pass of the hot path over one batch of synthetic input:
   c5: one full EGGROLL training step (config 5): 12,288 pairs = 24,576 members over an 8 x 2048 batch, chunks of
       512 members, fitness, outer-product gradient assembly and AdamW. 50,331,648 member-tokens.
 The JSON line carries the metric of BASELINE.json, the roofline of the dominant kernel (HIP events on the launch
-stream over the timed region), the oracle's CPU throughput on a bounded sample, and the credit readout's TFLOP/s at
-config 3 (B16 H8 T2048 d64). `roofline.traffic` is the dominant kernel's HBM bytes per launch as recorded in
+stream over the timed region), the oracle's CPU throughput on a bounded sample, the credit readout's TFLOP/s at
+config 3 (B16 H8 T2048 d64), and the time of Dust's head-slab estimator at the reference recipe's per-GPU draws. `roofline.traffic` is the dominant kernel's HBM bytes per launch as recorded in
 profiles/population_forward_c4_traffic.txt (rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this script, each scaled
 by what the counter reads for --copy-calibration); it is null for a workload or kernel that file does not cover.
 """
@@ -258,6 +258,32 @@ def bench_credit(dev, iters=10):
     return out
 
 
+def bench_head_error(dev, iters=3):
+    """Dust's head-slab CE estimator (train/val/dust.py:261-303) at the reference recipe's per-GPU head draws
+    (recipe(1.5).head = 73,728 over 8 GPUs = 9,216, nrep 16) over an 8 x 2048 token batch, vocabulary 4096."""
+    import torch
+    from noise_amd import _lib, dust
+    b, t, V, draws = 8, 2048, 4096, 9216
+    g = torch.Generator(device=dev).manual_seed(0)
+    raw = (3.0 * torch.randn(b, t, V, device=dev, generator=g)).bfloat16()
+    y = torch.randint(0, V, (b, t), device=dev, generator=g)
+    clean = 8.0 + torch.randn(b, t, device=dev, generator=g)
+    dust.head_error(raw, y, clean, draws, sigma=0.1, nrep=16)
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    for _ in range(iters):
+        err = dust.head_error(raw, y, clean, draws, sigma=0.1, nrep=16)
+    torch.cuda.synchronize()
+    tm = _lib.timing_read()
+    _lib.timing_enable(False)
+    ms = tm['head_error'][1] / tm['head_error'][0]
+    jittered = draws * b * t * 256
+    return dict(ms=round(ms, 3), draws=draws, token_rows=b * t, vocab=V, finite=bool(torch.isfinite(err).all()),
+                jittered_logits_per_s=round(jittered / (ms * 1e-3), 1),
+                note='per call: 9,216 draws x 16,384 token rows x one 256-column slab, the jitter regenerated '
+                     'twice from the counter stream (loss, then error), never stored')
+
+
 def cpu_baseline(model, sample_members=4, T=T_SEQ, reps=3):
     """The oracle (fp32 eager torch on the host cores) on a bounded sample of the same population forward."""
     import torch
@@ -303,6 +329,7 @@ def main():
     ap.add_argument('--workload', choices=['c4', 'c5'], default='c4')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-credit', action='store_true')
+    ap.add_argument('--no-dust', action='store_true', help="skip the head-slab estimator's line")
     ap.add_argument('--copy-calibration', action='store_true',
                     help='run one plain device copy of exactly 1 GiB and exit (rocprofv3 counter calibration)')
     args = ap.parse_args()
@@ -329,6 +356,8 @@ def main():
     line['finite'] = res['finite']
     if not args.no_credit:
         line['credit'] = bench_credit(dev)
+    if not args.no_dust:
+        line['dust_head_error'] = bench_head_error(dev)
     if not args.no_cpu_baseline:
         line['cpu_baseline'] = cpu_baseline(model)
     print(json.dumps(line), flush=True)

@@ -167,6 +167,23 @@ int noise_credit_key_context(const uint16_t* q, const uint16_t* k, const uint16_
 int noise_credit_value(const uint16_t* q, const uint16_t* k, const float* lse, const float* src, int64_t rows,
                        int64_t T, int32_t window, int32_t hi_lo, float* out, void* stream);
 
+/* ---- next row: Dust's head-slab CE estimator --------------------------------------------------------------- */
+
+/* error[r, v] (fp32 [b * t, ld], rows r = bi * t + ti) = per-token error estimates of the lm_head outputs raw (bf16
+ * [b * t, ld], the clean forward's, before the soft cap): chunk c of n draws (n = the largest count <= nrep that
+ * divides draws) jitters vocabulary slab c % (vocab / 256) by sigma a (this library's counter-based Gaussians,
+ * streamed by seed, draw and row), recomputes each token's soft-capped CE from the cached sums of the other slabs,
+ * rewards clean_loss - CE (0 where targets == -1; centered over the batch when b > 1), and error of the slab's columns
+ * = -(sum over its draws of reward / sigma * a) / (draws per slab); columns from vocab to ld are 0.
+ * vocab % 256 == 0, vocab <= ld, ld % 4 == 0, (draws / n) % (vocab / 256) == 0, draws <= 65535, b * t <= 2^26.
+ * Workspace: noise_head_error_workspace(b * t, vocab, draws) bytes.
+ * Replaces: train/val/dust.py:261-303 (DUST.head_error), with its torch.randn jitter (dust.py:192-193) replaced by the
+ * counter stream. */
+int noise_head_error(const uint16_t* raw, int64_t ld, const int64_t* targets, const float* clean_loss, int32_t b,
+                     int32_t t, int32_t vocab, int32_t draws, int32_t nrep, float sigma, uint64_t seed, float* error,
+                     void* workspace, size_t workspace_bytes, void* stream);
+size_t noise_head_error_workspace(int64_t rows, int32_t vocab, int32_t draws);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,7 @@ namespace noise {
 
 constexpr uint32_t kStreamBuffer = 0x4E4F4953u;
 constexpr uint32_t kStreamOffset = 0x4F464653u;
+constexpr uint32_t kStreamHead = 0x44414548u;  // the head-slab estimator's per-draw logit jitter
 constexpr uint64_t kNoiseSize = 1ull << 28;
 
 struct u32x4s { uint32_t x, y, z, w; };
@@ -103,6 +104,15 @@ __device__ __forceinline__ float buffer_value(uint64_t seed, uint64_t i) {
   buffer_quad(seed, i >> 2, z);
   const uint32_t lane = (uint32_t)(i & 3);
   return lane == 0 ? z[0] : lane == 1 ? z[1] : lane == 2 ? z[2] : z[3];
+}
+
+// Jitter of the head-slab estimator: four Gaussians for draw g, token row r, columns 4 q .. 4 q + 3 (q < 64) of the
+// jittered 256-column slab: philox(ctr = (64 r + q, g, 0, kStreamHead), key = seed), Box-Muller as above.
+// Replaces the estimator's torch.randn draws (train/val/dust.py:192-193, 281).
+__device__ __forceinline__ void head_noise_quad(uint64_t seed, uint32_t draw, uint32_t row, uint32_t q, float z[4]) {
+  const u32x4s r = philox4x32_10(u32x4s{row * 64u + q, draw, 0u, kStreamHead}, (uint32_t)seed, (uint32_t)(seed >> 32));
+  box_muller(r.x, r.y, &z[0], &z[1]);
+  box_muller(r.z, r.w, &z[2], &z[3]);
 }
 
 __device__ __forceinline__ int64_t offset_value(uint64_t seed, uint64_t step, uint32_t param, uint32_t direction,

@@ -36,6 +36,8 @@ def lib():
                                               ctypes.c_int64, ctypes.c_void_p]
         _lib.oracle_noise_rows.argtypes = [ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                            ctypes.c_void_p]
+        _lib.oracle_head_noise.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int64,
+                                           ctypes.c_void_p]
     return _lib
 
 
@@ -93,3 +95,10 @@ def philox_numpy(c0, c1, c2, c3, k0, k1):
         k0 = np.uint32((int(k0) + int(W0)) & 0xFFFFFFFF)
         k1 = np.uint32((int(k1) + int(W1)) & 0xFFFFFFFF)
     return c
+
+
+def head_noise(seed, draw, row0, n):
+    """float32 [n, 256]: the head-slab estimator's jitter of one draw at token rows row0 .. row0 + n - 1."""
+    out = np.empty((n, 256), np.float32)
+    lib().oracle_head_noise(seed, draw, row0, n, out.ctypes.data)
+    return out

@@ -68,3 +68,11 @@ def _state(cfg):
     m = GPT(cfg)
     m.init_weights()
     return m.state_dict()
+
+
+def test_head_error_takes_device_tensors_only():
+    from noise_amd import dust
+    raw = torch.zeros(1, 4, 256)
+    with pytest.raises(ValueError):
+        dust.head_error(raw, torch.zeros(1, 4, dtype=torch.long), torch.zeros(1, 4), draws=16)
+    assert dust.chunk_size(48, 16) == 16 and dust.chunk_size(24, 16) == 12 and dust.chunk_size(7, 16) == 7

@@ -1,0 +1,81 @@
+"""The head-slab estimator's oracle (oracle/dust.py, train/val/dust.py:261-303) pinned by identities it must meet,
+independent of its own code: the slab bookkeeping of the partition function against a dense log-sum-exp, and Stein's
+lemma, E[-(reward / sigma) a] -> (1 - 1/b) dCE/draw for small sigma (the centering over the batch removes 1/b of a
+row's own term), with the analytic gradient of the soft-capped CE."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dust as od
+from oracle import rng
+
+
+def _raw(b, t, V, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (3.0 * torch.randn(b, t, V, generator=g)).to(torch.bfloat16).float()
+
+
+def test_jitter_is_standard_normal_and_distinct_per_draw_and_row():
+    a = np.stack([rng.head_noise(11, d, 0, 64) for d in range(8)])  # [8 draws, 64 rows, 256]
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1) < 0.01
+    flat = a.reshape(8 * 64, 256)
+    c = np.corrcoef(flat[:64])
+    assert np.abs(c - np.eye(64)).max() < 0.3  # rows of one draw independent
+    assert not np.array_equal(a[0], a[1])
+    assert np.array_equal(rng.head_noise(11, 3, 5, 4), a[3, 5:9])  # a row's values do not depend on the batch start
+
+
+def test_partition_bookkeeping_equals_dense_logsumexp():
+    b, t, V, sigma = 2, 3, 768, 0.5
+    raw = _raw(b, t, V, 1)
+    z = 15 * torch.tanh(raw.double() / 15)
+    slab_sums = z.exp().view(b, t, 3, 256).sum(-1)
+    total = slab_sums.sum(-1)
+    a = od.jitter(7, 0, b, t).double()
+    for block in range(3):
+        lo = block * 256
+        changed = 15 * torch.tanh((raw[..., lo:lo + 256].double() + sigma * a) / 15)
+        part = (total - slab_sums[..., block]) + changed.exp().sum(-1)
+        dense = z.clone()
+        dense[..., lo:lo + 256] = changed
+        assert torch.allclose(part.log(), torch.logsumexp(dense, -1), rtol=1e-12, atol=1e-12)
+
+
+def _grad(raw, y, vocab):
+    z = 15 * torch.tanh(raw[..., :vocab].double() / 15)
+    g = torch.softmax(z, -1)
+    g.scatter_add_(-1, y.clamp(min=0).unsqueeze(-1), -torch.ones(*y.shape, 1, dtype=torch.float64))
+    g = g * (1 - torch.tanh(raw[..., :vocab].double() / 15) ** 2)
+    return torch.where((y != -1).unsqueeze(-1), g, torch.zeros(()))
+
+
+@pytest.mark.parametrize('b', [1, 2])
+def test_estimate_tends_to_scaled_gradient(b):
+    t, V, sigma = 2, 512, 0.01
+    draws = 2 * 2048  # 2048 draws per slab
+    raw = _raw(b, t, V, 2) * 0.5
+    g = torch.Generator().manual_seed(3)
+    y = torch.randint(0, V, (b, t), generator=g)
+    if b > 1:
+        y[1, 1] = -1  # an ignored target
+    clean = od.soft_capped_ce(raw, y)
+    est = od.head_error(raw, y, clean, draws, sigma=sigma, nrep=16, seed=5)
+    expect = (1 - 1 / b) * _grad(raw, y, V) if b > 1 else _grad(raw, y, V)
+    # b = 1: no centering; the estimator's standard error is about ||g|| / sqrt(draws per slab)
+    err = (est.double() - expect).abs().max().item()
+    assert err < 5 / math.sqrt(2048), err
+    # the target columns carry the large gradient entries: their estimates have the right sign and size
+    for bi in range(b):
+        for ti in range(t):
+            if y[bi, ti] >= 0:
+                e, x = est[bi, ti, y[bi, ti]].item(), expect[bi, ti, y[bi, ti]].item()
+                assert x < 0 and abs(e - x) < 0.15 * abs(x) + 0.05, (e, x)
+
+
+def test_chunks_must_cover_slabs():
+    raw = _raw(1, 1, 512)
+    y = torch.zeros(1, 1, dtype=torch.long)
+    with pytest.raises(ValueError):
+        od.head_error(raw, y, od.soft_capped_ce(raw, y), draws=16, nrep=16)  # 1 chunk, 2 slabs
