@@ -167,7 +167,49 @@ int noise_credit_key_context(const uint16_t* q, const uint16_t* k, const uint16_
 int noise_credit_value(const uint16_t* q, const uint16_t* k, const float* lse, const float* src, int64_t rows,
                        int64_t T, int32_t window, int32_t hi_lo, float* out, void* stream);
 
-/* ---- next row: Dust's head-slab CE estimator --------------------------------------------------------------- */
+/* ---- next rows: Dust's direct draws and head-slab CE estimator ----------------------------------------------- */
+
+/* One chunk of direct draws (train/val/dust.py:210-259): n_draws draws of the batch's n_seq sequences, member m =
+ * (draw draw0 + m / n_seq, batch row m % n_seq), each adding sigma a (this library's counter-based Gaussians, by seed,
+ * draw, site and token row) at the chosen sites of block `entry` and rerunning the network from there. */
+typedef struct noise_dust_draws {
+  int32_t entry;      /* the jittered block; -1: the token embedding (every block reruns, from the embedding) */
+  const float* x_in;  /* entry >= 0: fp32 [n_seq, T, 512], the captured (mixed) input of block `entry` */
+  const float* x0_in; /* entry >= 0: fp32 [n_seq, T, 512], the captured x0 = norm(embedding) */
+  int32_t sites;      /* bit s jitters site s: 0 the token embedding (entry -1); 1 the attention output (before
+                         attn.c_proj), 2 attn.c_proj's output, 3 mlp.c_fc's output, 4 mlp.c_proj's output */
+  float sigma;
+  uint64_t seed;
+  int32_t draw0;      /* global index of the chunk's first draw (the jitter stream's draw counter) */
+  int32_t n_draws;
+} noise_dust_draws;
+
+/* The clean pass (dust.py:195-208, DUST.capture): token_loss fp32 [n_seq, T] (per-token CE, 0 where targets == -1) and
+ * capture fp32 [n_layer + 1, n_seq, T, 512]: the mixed input of every block (the blocks' forward pre-hooks), then x0.
+ * tokens, targets int64 [n_seq, T]; T % 128 == 0. Workspace: noise_dust_workspace(1, n_seq, T).
+ * Replaces: train/val/dust.py:176-208 (the capture hooks and DUST.capture's clean losses). */
+int noise_dust_capture(const noise_gpt* model, const int64_t* tokens, const int64_t* targets, int64_t n_seq,
+                       int64_t T, float* token_loss, float* capture, void* workspace, size_t workspace_bytes,
+                       void* stream);
+/* Per-token CE of the chunk's draws, token_loss fp32 [n_draws, n_seq, T], clean weights.
+ * Workspace: noise_dust_workspace(n_draws, n_seq, T).
+ * Replaces: train/val/dust.py:210-233 (DUST.rerun with block_forward's jitter sites, :104-120, and head_loss,
+ * :94-99), its torch.randn jitter (:192-193, 244) replaced by the counter stream. */
+int noise_dust_rerun(const noise_gpt* model, const noise_dust_draws* draws, const int64_t* tokens,
+                     const int64_t* targets, int64_t n_seq, int64_t T, float* token_loss, void* workspace,
+                     size_t workspace_bytes, void* stream);
+size_t noise_dust_workspace(int64_t n_draws, int64_t n_seq, int64_t T);
+/* One chunk's contribution to a site's error estimate (dust.py:246-257): reward[j] = clean_loss - token_loss[j],
+ * centered over the chunk's draws when n_draws > 1, then (gamma > 0) the decayed reward-to-go along T (dust.py:86-91);
+ * error fp32 [n_seq, T, width] -= sum_j reward[j] a_j / sigma, with a_j the draw's jitter at `site` regenerated from
+ * (seed, draw0 + j). The caller zeroes error before a site's first chunk and divides by the draw count after the last.
+ * Workspace: noise_dust_errors_workspace(n_draws, n_seq, T).
+ * Replaces: train/val/dust.py:235-259 (DUST.direct_errors' reward and einsum). */
+int noise_dust_errors(const float* token_loss, const float* clean_loss, int32_t n_draws, int64_t n_seq, int64_t T,
+                      float gamma, float sigma, uint64_t seed, int32_t draw0, int32_t site, int32_t width,
+                      float* error, void* workspace, size_t workspace_bytes, void* stream);
+size_t noise_dust_errors_workspace(int32_t n_draws, int64_t n_seq, int64_t T);
+
 
 /* error[r, v] (fp32 [b * t, ld], rows r = bi * t + ti) = per-token error estimates of the lm_head outputs raw (bf16
  * [b * t, ld], the clean forward's, before the soft cap): chunk c of n draws (n = the largest count <= nrep that

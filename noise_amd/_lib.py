@@ -34,6 +34,11 @@ class NoisePerturbation(ctypes.Structure):
                                      ('c_q', 'c_k', 'c_v', 'c_proj', 've_gate', 'c_fc', 'mlp_proj', 've')]
 
 
+class NoiseDustDraws(ctypes.Structure):
+    _fields_ = [('entry', i32), ('x_in', c_p), ('x0_in', c_p), ('sites', i32), ('sigma', f32), ('seed', u64),
+                ('draw0', i32), ('n_draws', i32)]
+
+
 _SIGNATURES = {
     'noise_last_error': ([], ctypes.c_char_p),
     'noise_abi_version': ([], ctypes.c_int),
@@ -57,6 +62,12 @@ _SIGNATURES = {
     'noise_credit_key_context': ([c_p, c_p, c_p, c_p, i64, i64, i32, c_p, c_p, c_p], ctypes.c_int),
     'noise_head_error': ([c_p, i64, c_p, c_p, i32, i32, i32, i32, i32, f32, u64, c_p, c_p, szt, c_p], ctypes.c_int),
     'noise_head_error_workspace': ([i64, i32, i32], szt),
+    'noise_dust_capture': ([ctypes.POINTER(NoiseGpt), c_p, c_p, i64, i64, c_p, c_p, c_p, szt, c_p], ctypes.c_int),
+    'noise_dust_rerun': ([ctypes.POINTER(NoiseGpt), ctypes.POINTER(NoiseDustDraws), c_p, c_p, i64, i64, c_p, c_p, szt,
+                          c_p], ctypes.c_int),
+    'noise_dust_workspace': ([i64, i64, i64], szt),
+    'noise_dust_errors': ([c_p, c_p, i32, i64, i64, f32, f32, u64, i32, i32, i32, c_p, c_p, szt, c_p], ctypes.c_int),
+    'noise_dust_errors_workspace': ([i32, i64, i64], szt),
 }
 
 EXPORTS = tuple(_SIGNATURES)

@@ -193,7 +193,7 @@ int noise_set_error(int code, const char* fmt, ...);
 // pairs recorded on their stream; noise_timing_read() reports counts and summed durations per class.
 enum NoiseTimingClass {
   kTimeNoise = 0, kTimeEmbed, kTimeNorm, kTimeQKV, kTimeRope, kTimeAttention, kTimeProj, kTimeFc, kTimeRowdot,
-  kTimeMlpProj, kTimeHead, kTimeCeFinal, kTimeCreditLse, kTimeCreditValue, kTimeUpdate, kTimeLowrank, kTimeCreditCenter, kTimeHeadError,
+  kTimeMlpProj, kTimeHead, kTimeCeFinal, kTimeCreditLse, kTimeCreditValue, kTimeUpdate, kTimeLowrank, kTimeCreditCenter, kTimeHeadError, kTimeDustRerun, kTimeDustErrors,
   kTimeClasses
 };
 

@@ -1,5 +1,9 @@
-// Dust's head-slab CE estimator (train/val/dust.py:261-303, DUST.head_error): per-token error estimates of the
-// lm_head outputs from draws that jitter one 256-column vocabulary slab at a time.
+// Dust's estimators that need no forward pass of their own: the head-slab CE estimator (train/val/dust.py:261-303,
+// DUST.head_error), and the reward and error sums of the direct draws (dust.py:235-259, DUST.direct_errors; their
+// reruns are the population forward's kernels, forward.hip noise_dust_rerun).
+//
+// Head-slab estimator: per-token error estimates of the lm_head outputs from draws that jitter one 256-column
+// vocabulary slab at a time.
 //
 // For chunk c of n draws (n = the largest count <= nrep dividing draws) the jittered slab is c % slabs. Draw g of the
 // chunk changes the slab's capped logits to 15 tanh((raw + sigma a_g) / 15) and recomputes the token's CE from the
@@ -13,6 +17,11 @@
 //   head_center_kernel  one thread per (draw, position): rewards, centered over the batch
 //   head_accum_kernel   one wave per (row, slab): the draws of that slab regenerate their jitter, the error sum
 // The jitter is this library's counter stream (rng.h head_noise_quad), never stored.
+//
+// Direct draws, per chunk of n draws: dust_reward_kernel (clean minus perturbed per-token loss, centered over the
+// draws), dust_rtg_kernel (gamma > 0: the decayed reward-to-go along the sequence), dust_accum_kernel (one thread per
+// token row and 4 channels of the site: the n draws' jitter regenerated (rng.h dust_noise_quad), error -= sum of
+// reward / sigma * a).
 #include <math.h>
 
 #include "common.h"
@@ -145,6 +154,61 @@ __global__ __launch_bounds__(256) void head_accum_kernel(const float* __restrict
                               -acc[3] * inv_per_slab};
 }
 
+// reward[j, r] = clean[r] - loss[j, r], minus its mean over the chunk's n draws (n > 1) (dust.py:246-249)
+__global__ __launch_bounds__(256) void dust_reward_kernel(const float* __restrict__ loss, const float* __restrict__ clean,
+                                                          int n, int64_t rows, float* __restrict__ reward) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const float c = clean[r];
+  float mean = 0.f;
+  for (int j = 0; j < n; ++j) {
+    const float rw = c - loss[(int64_t)j * rows + r];
+    reward[(int64_t)j * rows + r] = rw;
+    mean += rw;
+  }
+  if (n > 1) {
+    mean /= (float)n;
+    for (int j = 0; j < n; ++j) reward[(int64_t)j * rows + r] -= mean;
+  }
+}
+
+// out[s, t] = sum_{k < lags, t + k < T} gamma^k reward[s, t + k] for each of the n_seqs sequences (dust.py:86-91)
+__global__ __launch_bounds__(256) void dust_rtg_kernel(const float* __restrict__ reward, int64_t n_seqs, int T,
+                                                       float gamma, int lags, float* __restrict__ out) {
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= n_seqs * T) return;
+  const int64_t s = id / T;
+  const int t = (int)(id % T);
+  const float* r = reward + s * T;
+  float acc = 0.f, g = 1.f;
+  for (int k = 0; k < lags && t + k < T; ++k) {
+    acc += g * r[t + k];
+    g *= gamma;
+  }
+  out[id] = acc;
+}
+
+// error[r, 4 q ..] -= sum_j reward[j, r] / sigma * a_j[r, 4 q ..]: one thread per token row r and 4 channels q
+__global__ __launch_bounds__(256) void dust_accum_kernel(const float* __restrict__ reward, int n, int64_t rows,
+                                                         int quads, float sigma, uint64_t seed, int draw0,
+                                                         uint32_t site, float* __restrict__ error) {
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= rows * quads) return;
+  const int64_t r = id / quads;
+  const int q = (int)(id % quads);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < n; ++j) {
+    const float w = reward[(int64_t)j * rows + r] / sigma;
+    float a[4];
+    dust_noise_quad(seed, (uint32_t)(draw0 + j), site, (uint32_t)r, (uint32_t)quads, (uint32_t)q, a);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] += w * a[k];
+  }
+  f32x4* e = (f32x4*)(error + r * (int64_t)quads * 4 + 4 * q);
+  const f32x4 old = *e;
+  *e = f32x4{old[0] - acc[0], old[1] - acc[1], old[2] - acc[2], old[3] - acc[3]};
+}
+
 static inline size_t al256h(size_t n) { return (n + 255) & ~(size_t)255; }
 
 static int chunk_of(int draws, int cap) {
@@ -204,6 +268,47 @@ extern "C" int noise_head_error(const uint16_t* raw, int64_t ld, const int64_t* 
   const int64_t waves = rows * n_slab_ld;
   hipLaunchKernelGGL(head_accum_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, loss, rows, ld, slabs,
                      n_slab_ld, n, chunks, sigma, 1.0f / (float)(draws / slabs), seed, error);
+  NOISE_LAUNCH_CHECK();
+  return NOISE_OK;
+}
+
+extern "C" size_t noise_dust_errors_workspace(int32_t n_draws, int64_t n_seq, int64_t T) {
+  if (n_draws <= 0 || n_seq <= 0 || T <= 0) return 0;
+  return 2 * al256h((size_t)n_draws * n_seq * T * 4);
+}
+
+extern "C" int noise_dust_errors(const float* token_loss, const float* clean_loss, int32_t n_draws, int64_t n_seq,
+                                 int64_t T, float gamma, float sigma, uint64_t seed, int32_t draw0, int32_t site,
+                                 int32_t width, float* error, void* workspace, size_t workspace_bytes,
+                                 void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  NOISE_REQUIRE(token_loss && clean_loss && error, "NULL pointer argument");
+  NOISE_REQUIRE(n_draws > 0 && n_seq > 0 && T > 0 && draw0 >= 0, "n_draws, n_seq, T positive and draw0 >= 0 needed");
+  NOISE_REQUIRE(sigma > 0.f && gamma >= 0.f && gamma < 1.f, "sigma > 0 and 0 <= gamma < 1 needed");
+  NOISE_REQUIRE(site >= 0 && site <= 4 && width > 0 && width % 4 == 0, "site %d outside [0, 4] or width %d not a "
+                "positive multiple of 4", site, width);
+  const int64_t rows = n_seq * T;
+  NOISE_REQUIRE(rows * (width / 4) <= ((int64_t)1 << 32) - 1, "rows * width / 4 exceeds the jitter counter");
+  NOISE_REQUIRE(workspace && workspace_bytes >= noise_dust_errors_workspace(n_draws, n_seq, T), "workspace too small");
+  float* reward = (float*)workspace;
+  float* rtg = (float*)((char*)workspace + al256h((size_t)n_draws * rows * 4));
+  NoiseTimer tm(kTimeDustErrors, stream);
+  hipLaunchKernelGGL(dust_reward_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, token_loss,
+                     clean_loss, n_draws, rows, reward);
+  NOISE_LAUNCH_CHECK();
+  const float* w = reward;
+  if (gamma > 0.f) {
+    const int lags = (int)ceil(log(1e-6) / log((double)gamma));
+    const int64_t n_el = (int64_t)n_draws * rows;
+    hipLaunchKernelGGL(dust_rtg_kernel, dim3((unsigned)((n_el + 255) / 256)), dim3(256), 0, stream, reward,
+                       (int64_t)n_draws * n_seq, (int)T, gamma, lags, rtg);
+    NOISE_LAUNCH_CHECK();
+    w = rtg;
+  }
+  const int quads = width / 4;
+  const int64_t threads = rows * quads;
+  hipLaunchKernelGGL(dust_accum_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, w, n_draws,
+                     rows, quads, sigma, seed, draw0, (uint32_t)site, error);
   NOISE_LAUNCH_CHECK();
   return NOISE_OK;
 }

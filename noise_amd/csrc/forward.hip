@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include "gemm.h"
+#include "rng.h"
 #include "window_flash.h"
 
 namespace noise {
@@ -31,10 +32,30 @@ struct Members {
   }
 };
 
+// Activation jitter of the direct draws (train/val/dust.py:210-233): sigma a added at one site of the entry block.
+// Members are (draw, batch row) pairs in draw-major order, so member m is draw draw0 + m / n_seq of batch row seq[m];
+// the jitter of (draw, site, token row, 4 channels) comes from the counter stream (rng.h dust_noise_quad).
+struct Jitter {
+  float sigma;  // 0: no jitter
+  uint32_t site;
+  uint64_t seed;
+  int draw0, n_seq;
+  __host__ __device__ __forceinline__ bool on() const { return sigma != 0.f; }
+  // sigma a at member row r, channels c .. c + 3 of a site `width` wide
+  __device__ __forceinline__ f32x4 quad(const Members& mb, int64_t r, int width, int c) const {
+    const int m = mb.member(r);
+    const uint32_t row = (uint32_t)((int64_t)mb.seq[m] * mb.T + (r - (int64_t)m * mb.T));
+    float z[4];
+    dust_noise_quad(seed, (uint32_t)(draw0 + m / n_seq), site, row, (uint32_t)(width / 4), (uint32_t)(c / 4), z);
+    return f32x4{sigma * z[0], sigma * z[1], sigma * z[2], sigma * z[3]};
+  }
+};
+
 // ---------------------------------------------------------------------------------------------------------------
-// x0 = norm(wte[tok] + sign a[tok] b)  (eggroll.py:61-63, 74); one wave per row, 8 channels per lane.
+// x0 = norm(wte[tok] + sign a[tok] b [+ the direct draws' jitter])  (eggroll.py:61-63, 74; dust.py:218-220); one wave
+// per row, 8 channels per lane.
 __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __restrict__ wte, int Vp, int64_t off_wte,
-                                                    float* __restrict__ x0, int64_t M) {
+                                                    Jitter jit, float* __restrict__ x0, int64_t M) {
   const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= M) return;
   const int lane = threadIdx.x & 63, c0 = lane * 8;
@@ -50,8 +71,17 @@ __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __r
   for (int j = 0; j < 8; ++j) {
     e[j] = wte[tok * kD + c0 + j];
     if (nr) e[j] += at * nr[off_wte + Vp + c0 + j];
-    ss += e[j] * e[j];
   }
+  if (jit.on()) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 z = jit.quad(mb, r, kD, c0 + 4 * h);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[4 * h + j] += z[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += e[j] * e[j];
   ss = warp_sum(ss);
   const float inv = bad ? __builtin_nanf("") : rsqrtf(ss * (1.0f / kD) + kNormEps);
   float* dst = x0 + r * kD + c0;
@@ -326,7 +356,7 @@ struct EpiQKV {
 // holds whole 512-wide rows (512-column tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3. Groups of
 // 4 rows keep the x and x0 prefetch small. The rank-1 term is added unconditionally: its a and dot are zero for rows
 // without noise.
-template <bool kMix, int kNDot>
+template <bool kMix, int kNDot, bool kJit = false>
 struct EpiResidNorm {
   static constexpr int kRows = 4;
   Members mb;
@@ -342,6 +372,7 @@ struct EpiResidNorm {
   bf16_t* h;            // [M, 512]
   int64_t off_b[3];     // noise offsets of the next linear's b vectors (kNDot of them)
   float* xb;            // [M, 4]
+  Jitter jit;           // kJit: the direct draws' jitter of this projection's output
   struct Wave {
     int row_base;
     const float* nr;
@@ -394,6 +425,12 @@ struct EpiResidNorm {
                                        f32x4 (&v)[R][2]) const {
     static_assert(R == 4, "warp_sum4 reduces 4 rows");
     const int i0 = row0 - w.row_base;
+    if constexpr (kJit) {
+#pragma unroll
+      for (int q = 0; q < R; ++q)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) v[q][hh] += jit.quad(mb, row0 + q, kD, hh * 256 + 4 * lane);
+    }
     float ss[R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
@@ -445,7 +482,8 @@ struct EpiResidNorm {
 
 // hidden = relu(acc + s (x . b) a)^2 in bf16 (utils/model.py:107), and the next linear's rank-1 partial dot
 // hidden . b_next over this 256-column tile (xb_next[row, n_tile]).
-struct EpiReluSq {
+template <bool kJit>
+struct EpiReluSqT {
   Members mb;
   bf16_t* out;
   int64_t ldo;
@@ -455,6 +493,7 @@ struct EpiReluSq {
   int64_t off_next_b;   // noise offset of the next linear's b (its input is this output)
   float* xb_next;       // [M, n_tiles]
   int n_tiles;
+  Jitter jit;           // kJit: the direct draws' jitter of the pre-activation
   static constexpr int kRows = kEpiRows;
   struct Wave {
     int row_base;
@@ -480,6 +519,10 @@ struct EpiReluSq {
   template <int R>
   __device__ __forceinline__ void rows(int row0, int n0, int n_tile, int lane, const Wave& w, const Pre&,
                                        f32x4 (&v)[R]) const {
+    if constexpr (kJit) {
+#pragma unroll
+      for (int q = 0; q < R; ++q) v[q] += jit.quad(mb, row0 + q, kF, n0 + 4 * lane);
+    }
     if (w.nr) {
 #pragma unroll
       for (int q = 0; q < R; ++q) {
@@ -510,6 +553,7 @@ struct EpiReluSq {
     }
   }
 };
+using EpiReluSq = EpiReluSqT<false>;
 
 // logits z = 15 tanh((acc + s (h . b) a) / 15) (utils/model.py:203-204) and, per row of this 256-column tile, the sum
 // over columns < vocab of exp(z - 15), plus the target's logit (utils/model.py:206-209). The soft cap keeps |z| < 15,
@@ -651,6 +695,24 @@ static Workspace carve(void* base, int64_t M) {
   return w;
 }
 
+// dst[r] = src[the member's batch row, same position]: the captured block input replicated over the draws
+__global__ __launch_bounds__(256) void replicate_rows_kernel(Members mb, const float* __restrict__ src,
+                                                             float* __restrict__ dst, int64_t M) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= M) return;
+  const int lane = threadIdx.x & 63, m = mb.member(r);
+  const float* s = src + ((int64_t)mb.seq[m] * mb.T + (r - (int64_t)m * mb.T)) * kD + lane * 8;
+  float* d = dst + r * kD + lane * 8;
+  *(f32x4*)d = *(const f32x4*)s;
+  *(f32x4*)(d + 4) = *(const f32x4*)(s + 4);
+}
+
+// member m of the direct draws: batch row m % n_seq (members are draw-major)
+__global__ void member_rows_kernel(int32_t* __restrict__ seq, int64_t members, int64_t n_seq) {
+  const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (m < members) seq[m] = (int32_t)(m % n_seq);
+}
+
 static bool g_prepared = false;
 static int prepare_all() {
   if (g_prepared) return NOISE_OK;
@@ -658,6 +720,9 @@ static int prepare_all() {
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<false, 1>>()));
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3>>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiReluSq>()));
+  NOISE_CHECK_HIP((prepare_gemm<Tile, EpiReluSqT<true>>()));
+  NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<false, 1, true>>()));
+  NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiHeadCE>()));
   g_prepared = true;
   return NOISE_OK;
@@ -672,12 +737,34 @@ extern "C" size_t noise_population_forward_workspace(int64_t members, int64_t T)
   return carve(nullptr, members * T).bytes;
 }
 
-extern "C" int noise_population_forward(const noise_gpt* model, const noise_perturbation* pert, const int64_t* tokens,
-                                        const int64_t* targets, int64_t n_seq, int64_t T, const int32_t* member_seq,
-                                        const int32_t* member_row, const float* member_sign, int64_t members,
-                                        float* loss_sum, float* token_loss, float* logits, void* workspace,
-                                        size_t workspace_bytes, void* stream_) {
-  hipStream_t stream = (hipStream_t)stream_;
+// The direct draws' part of a forward (train/val/dust.py:195-233): a clean pass that captures every block's input
+// (capture != NULL), or a rerun of blocks entry .. n_layer - 1 from a captured input with jitter at sites of block
+// `entry` (entry -1: the token embedding's jitter, every block rerun).
+struct DustRun {
+  int entry;
+  const float* x_in;
+  const float* x0_in;
+  int sites;  // bit s: jitter site s (0 embedding, 1 attention output, 2 attn.c_proj, 3 mlp.c_fc, 4 mlp.c_proj)
+  float sigma;
+  uint64_t seed;
+  int draw0, n_seq;
+  float* capture;  // [n_layer + 1, M, 512]: block inputs, then x0
+  // the jitter of site s when it is set and block i is the entry
+  Jitter jit(int i, int s) const {
+    Jitter j;
+    memset(&j, 0, sizeof(j));
+    if (((sites >> s) & 1) && (s == 0 ? entry < 0 : i == entry)) {
+      j.sigma = sigma; j.site = (uint32_t)s; j.seed = seed; j.draw0 = draw0; j.n_seq = n_seq;
+    }
+    return j;
+  }
+};
+
+static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, const int64_t* tokens,
+                        const int64_t* targets, int64_t n_seq, int64_t T, const int32_t* member_seq,
+                        const int32_t* member_row, const float* member_sign, int64_t members, float* loss_sum,
+                        float* token_loss, float* logits, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                        const DustRun* dr) {
   NOISE_REQUIRE(model && pert, "model / perturbation is NULL");
   NOISE_REQUIRE(members > 0 && n_seq > 0, "members and n_seq must be positive");
   NOISE_REQUIRE(T > 0 && T % 128 == 0, "T = %lld must be a positive multiple of 128", (long long)T);
@@ -702,24 +789,39 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
   const int Vp = model->padded_vocab;
   const bool noisy = pert->rows != nullptr;
   const unsigned row_blocks = (unsigned)((M + 3) / 4);
+  DustRun none;
+  memset(&none, 0, sizeof(none));
+  none.entry = -1;
+  if (!dr) dr = &none;
+  const bool from_block = dr->entry >= 0;  // rerun from a captured block input
+  const int first_layer = from_block ? dr->entry : 0;
 
-  {
+  if (from_block) {
+    hipLaunchKernelGGL(replicate_rows_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, dr->x_in, ws.x, M);
+    NOISE_LAUNCH_CHECK();
+    hipLaunchKernelGGL(replicate_rows_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, dr->x0_in, ws.x0, M);
+    NOISE_LAUNCH_CHECK();
+  } else {
     NoiseTimer tm(kTimeEmbed, stream);
-    hipLaunchKernelGGL(embed_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte, ws.x0, M);
+    hipLaunchKernelGGL(embed_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte,
+                       dr->jit(-1, 0), ws.x0, M);
     NOISE_LAUNCH_CHECK();
   }
+  if (dr->capture)
+    NOISE_CHECK_HIP(hipMemcpyAsync(dr->capture + (int64_t)model->n_layer * M * kD, ws.x0, (size_t)M * kD * 4,
+                                   hipMemcpyDeviceToDevice, stream));
 
-  for (int i = 0; i < model->n_layer; ++i) {
+  for (int i = first_layer; i < model->n_layer; ++i) {
     const noise_layer& L = model->layers[i];
     NOISE_REQUIRE(L.w_qkv && L.w_proj && L.w_fc && L.w_mlp_proj, "layer %d weight pointer is NULL", i);
     NOISE_REQUIRE((L.w_gate == nullptr) == (L.ve == nullptr), "layer %d: w_gate and ve must both be set or both NULL", i);
     NOISE_REQUIRE(L.window >= 0, "layer %d: negative window", i);
-    if (i == 0) {
+    if (i == first_layer) {
       // lambda mix + norm + q/k/v dots + gate of the first block (later blocks get theirs from the epilogue of the
-      // previous block's MLP projection)
+      // previous block's MLP projection); a rerun from a captured block input starts from the mixed x: norm only
       NormArgs na;
       memset(&na, 0, sizeof(na));
-      na.x = ws.x; na.x0 = ws.x0; na.mix = 1; na.first = 1;
+      na.x = ws.x; na.x0 = ws.x0; na.mix = from_block ? 0 : 1; na.first = from_block ? 0 : 1;
       na.resid_lambdas = model->resid_lambdas; na.x0_lambdas = model->x0_lambdas; na.layer = 0;
       na.off_resid = pert->resid_lambdas; na.off_x0 = pert->x0_lambdas;
       na.h = ws.h; na.ndot = 3;
@@ -734,6 +836,9 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
                          pert->ve_gate[i], ws.gate, M);
       NOISE_LAUNCH_CHECK();
     }
+    if (dr->capture)  // x now holds block i's (mixed) input
+      NOISE_CHECK_HIP(hipMemcpyAsync(dr->capture + (int64_t)i * M * kD, ws.x, (size_t)M * kD * 4,
+                                     hipMemcpyDeviceToDevice, stream));
 
     EpiQKV eq{mb, ws.qkv, {pert->c_q[i], pert->c_k[i], pert->c_v[i]}, ws.xb, L.w_gate ? ws.gate : nullptr, L.ve,
               pert->ve[i], Vp, model->rope_cos, model->rope_sin};
@@ -753,6 +858,11 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     fa.heads = kH; fa.T = (int)T; fa.window = L.window;
     fa.bound = 8.0f;  // q and k are RMS-normed over 64 channels: |q . k| / 8 <= 8
     {
+      const Jitter jo = dr->jit(i, 1);
+      fa.jit_sigma = jo.sigma; fa.jit_site = jo.site; fa.jit_seed = jo.seed; fa.jit_draw0 = jo.draw0;
+      fa.jit_n_seq = jo.n_seq > 0 ? jo.n_seq : 1; fa.jit_seq = member_seq;
+    }
+    {
       NoiseTimer tm(kTimeAttention, stream);
       NOISE_CHECK_HIP((launch_flash<kAttn, true, kAttnOG>(fa, members, kH, stream)));
     }
@@ -765,13 +875,27 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     ep.xb = ws.xb;
     {
       NoiseTimer tm(kTimeProj, stream);
-      NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
+      const Jitter jp = dr->jit(i, 2);
+      if (jp.on()) {
+        EpiResidNorm<false, 1, true> ej;
+        memcpy((void*)&ej, (const void*)&ep, sizeof(ep));
+        ej.jit = jp;
+        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ej, stream)));
+      } else {
+        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
+      }
     }
 
-    EpiReluSq er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4, pert->mlp_proj[i] + kD, ws.xb1, kF / Tile::BN};
     {
       NoiseTimer tm(kTimeFc, stream);
-      NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
+      const Jitter jf = dr->jit(i, 3);
+      if (jf.on()) {
+        EpiReluSqT<true> er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4, pert->mlp_proj[i] + kD, ws.xb1, kF / Tile::BN, jf};
+        NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
+      } else {
+        EpiReluSq er{mb, ws.hid, kF, pert->c_fc[i], ws.xb, 4, pert->mlp_proj[i] + kD, ws.xb1, kF / Tile::BN, Jitter{}};
+        NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
+      }
     }
 
     // MLP projection + residual, then the next block's lambda mix, norm and q/k/v dots (or the final norm and
@@ -783,7 +907,15 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
       em.mb = mb; em.x = ws.x; em.xbp = ws.xb1; em.nxb = kF / Tile::BN; em.off = pert->mlp_proj[i];
       em.h = ws.h; em.xb = ws.xb; em.off_b[0] = pert->lm_head + Vp;
       NoiseTimer tm(kTimeMlpProj, stream);
-      NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+      const Jitter jm = dr->jit(i, 4);
+      if (jm.on()) {
+        EpiResidNorm<false, 1, true> ej;
+        memcpy((void*)&ej, (const void*)&em, sizeof(em));
+        ej.jit = jm;
+        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, ej, stream)));
+      } else {
+        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+      }
     } else {
       EpiResidNorm<true, 3> em;
       memset(&em, 0, sizeof(em));
@@ -793,7 +925,15 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
       em.layer = i + 1; em.off_resid = pert->resid_lambdas; em.off_x0 = pert->x0_lambdas;
       em.off_b[0] = pert->c_q[i + 1] + kD; em.off_b[1] = pert->c_k[i + 1] + kD; em.off_b[2] = pert->c_v[i + 1] + kD;
       NoiseTimer tm(kTimeMlpProj, stream);
-      NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+      const Jitter jm = dr->jit(i, 4);
+      if (jm.on()) {
+        EpiResidNorm<true, 3, true> ej;
+        memcpy((void*)&ej, (const void*)&em, sizeof(em));
+        ej.jit = jm;
+        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, ej, stream)));
+      } else {
+        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
+      }
     }
   }
 
@@ -815,4 +955,76 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
     }
   }
   return NOISE_OK;
+}
+
+extern "C" int noise_population_forward(const noise_gpt* model, const noise_perturbation* pert, const int64_t* tokens,
+                                        const int64_t* targets, int64_t n_seq, int64_t T, const int32_t* member_seq,
+                                        const int32_t* member_row, const float* member_sign, int64_t members,
+                                        float* loss_sum, float* token_loss, float* logits, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return forward_impl(model, pert, tokens, targets, n_seq, T, member_seq, member_row, member_sign, members, loss_sum,
+                      token_loss, logits, workspace, workspace_bytes, (hipStream_t)stream, nullptr);
+}
+
+// ---- the direct draws (train/val/dust.py:195-233) ------------------------------------------------------------
+
+extern "C" size_t noise_dust_workspace(int64_t n_draws, int64_t n_seq, int64_t T) {
+  if (n_draws <= 0 || n_seq <= 0 || T <= 0) return 0;
+  const int64_t members = n_draws * n_seq;
+  return align256((size_t)members * 4) + carve(nullptr, members * T).bytes;
+}
+
+// members = n_draws * n_seq (draw-major, member m on batch row m % n_seq), clean weights; per-token CE out
+static int dust_forward(const noise_gpt* model, const int64_t* tokens, const int64_t* targets, int64_t n_seq, int64_t T,
+                        int64_t n_draws, float* token_loss, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                        const DustRun& dr) {
+  NOISE_REQUIRE(model && tokens && targets && token_loss, "NULL pointer argument");
+  NOISE_REQUIRE(n_seq > 0 && n_draws > 0 && T > 0, "n_seq, n_draws and T must be positive");
+  const int64_t members = n_draws * n_seq;
+  NOISE_REQUIRE(workspace && workspace_bytes >= noise_dust_workspace(n_draws, n_seq, T), "workspace too small");
+  int32_t* seq = (int32_t*)workspace;
+  const size_t head = align256((size_t)members * 4);
+  hipLaunchKernelGGL(member_rows_kernel, dim3((unsigned)((members + 255) / 256)), dim3(256), 0, stream, seq, members,
+                     n_seq);
+  NOISE_LAUNCH_CHECK();
+  noise_perturbation clean;
+  memset(&clean, 0, sizeof(clean));  // rows == NULL: no weight noise
+  if (!dr.capture) {
+    NoiseTimer tm(kTimeDustRerun, stream);
+    return forward_impl(model, &clean, tokens, targets, n_seq, T, seq, seq, (const float*)seq, members, nullptr,
+                        token_loss, nullptr, (char*)workspace + head, workspace_bytes - head, stream, &dr);
+  }
+  return forward_impl(model, &clean, tokens, targets, n_seq, T, seq, seq, (const float*)seq, members, nullptr,
+                      token_loss, nullptr, (char*)workspace + head, workspace_bytes - head, stream, &dr);
+}
+
+extern "C" int noise_dust_capture(const noise_gpt* model, const int64_t* tokens, const int64_t* targets, int64_t n_seq,
+                                  int64_t T, float* token_loss, float* capture, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  NOISE_REQUIRE(capture, "capture is NULL");
+  DustRun dr;
+  memset(&dr, 0, sizeof(dr));
+  dr.entry = -1; dr.n_seq = (int)n_seq; dr.capture = capture;
+  return dust_forward(model, tokens, targets, n_seq, T, 1, token_loss, workspace, workspace_bytes,
+                      (hipStream_t)stream, dr);
+}
+
+extern "C" int noise_dust_rerun(const noise_gpt* model, const noise_dust_draws* d, const int64_t* tokens,
+                                const int64_t* targets, int64_t n_seq, int64_t T, float* token_loss, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  NOISE_REQUIRE(model && d, "NULL pointer argument");
+  NOISE_REQUIRE(d->entry >= -1 && d->entry < model->n_layer, "entry %d outside [-1, n_layer)", d->entry);
+  NOISE_REQUIRE(d->n_draws > 0 && d->draw0 >= 0 && d->sigma >= 0.f, "n_draws > 0, draw0 >= 0, sigma >= 0 needed");
+  NOISE_REQUIRE(d->entry < 0 ? (d->sites & ~1) == 0 : (d->sites & ~0x1E) == 0,
+                "sites 0x%x do not belong to entry %d (embedding: bit 0; a block: bits 1-4)", d->sites, d->entry);
+  NOISE_REQUIRE(d->entry < 0 || (d->x_in && d->x0_in), "a rerun from block %d needs its captured input and x0",
+                d->entry);
+  NOISE_REQUIRE(n_seq <= (int64_t)1 << 20 && (int64_t)d->n_draws * n_seq * T <= (int64_t)INT32_MAX / 4,
+                "n_draws * n_seq * T too large");
+  DustRun dr;
+  memset(&dr, 0, sizeof(dr));
+  dr.entry = d->entry; dr.x_in = d->x_in; dr.x0_in = d->x0_in; dr.sites = d->sites; dr.sigma = d->sigma;
+  dr.seed = d->seed; dr.draw0 = d->draw0; dr.n_seq = (int)n_seq;
+  return dust_forward(model, tokens, targets, n_seq, T, d->n_draws, token_loss, workspace, workspace_bytes,
+                      (hipStream_t)stream, dr);
 }

@@ -16,6 +16,7 @@ namespace noise {
 constexpr uint32_t kStreamBuffer = 0x4E4F4953u;
 constexpr uint32_t kStreamOffset = 0x4F464653u;
 constexpr uint32_t kStreamHead = 0x44414548u;  // the head-slab estimator's per-draw logit jitter
+constexpr uint32_t kStreamDust = 0x54535544u;  // the direct draws' per-draw activation jitter
 constexpr uint64_t kNoiseSize = 1ull << 28;
 
 struct u32x4s { uint32_t x, y, z, w; };
@@ -111,6 +112,18 @@ __device__ __forceinline__ float buffer_value(uint64_t seed, uint64_t i) {
 // Replaces the estimator's torch.randn draws (train/val/dust.py:192-193, 281).
 __device__ __forceinline__ void head_noise_quad(uint64_t seed, uint32_t draw, uint32_t row, uint32_t q, float z[4]) {
   const u32x4s r = philox4x32_10(u32x4s{row * 64u + q, draw, 0u, kStreamHead}, (uint32_t)seed, (uint32_t)(seed >> 32));
+  box_muller(r.x, r.y, &z[0], &z[1]);
+  box_muller(r.z, r.w, &z[2], &z[3]);
+}
+
+// Jitter of the direct draws: four Gaussians for draw g at site s (0 token embedding, 1 attention output, 2 attention
+// projection, 3 MLP hidden, 4 MLP projection), token row r (batch row * T + position), channels 4 q .. 4 q + 3 of a
+// site `quads` * 4 channels wide: philox(ctr = (r * quads + q, g, s, kStreamDust), key = seed), Box-Muller as above.
+// Replaces the direct draws' torch.randn (train/val/dust.py:192-193, 244).
+__device__ __forceinline__ void dust_noise_quad(uint64_t seed, uint32_t draw, uint32_t site, uint32_t row,
+                                                uint32_t quads, uint32_t q, float z[4]) {
+  const u32x4s r =
+      philox4x32_10(u32x4s{row * quads + q, draw, site, kStreamDust}, (uint32_t)seed, (uint32_t)(seed >> 32));
   box_muller(r.x, r.y, &z[0], &z[1]);
   box_muller(r.z, r.w, &z[2], &z[3]);
 }

@@ -27,6 +27,7 @@
 #pragma once
 
 #include "common.h"
+#include "rng.h"
 
 namespace noise {
 
@@ -49,6 +50,13 @@ struct FlashArgs {
   int64_t xb_stride;
   int32_t heads, T, window, hi_lo;
   float bound;          // kAttn: > 0 when |x . y / 8| <= bound is guaranteed (fixed-reference softmax)
+  // kAttn: the direct draws' jitter of the output (jit_sigma 0: none). Batch entry b is draw jit_draw0 + b / jit_n_seq
+  // of token row jit_seq[b]; the jitter of output o, channel c of the heads * 64 comes from rng.h dust_noise_quad.
+  float jit_sigma;
+  uint32_t jit_site;
+  uint64_t jit_seed;
+  int32_t jit_draw0, jit_n_seq;
+  const int32_t* jit_seq;
 };
 
 constexpr int kFlashBI = 64;
@@ -421,15 +429,25 @@ __global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
         bf16_t* og_ptr = (bf16_t*)a.out + b * a.o_sb + (int64_t)my_o * a.o_st + head * 64;
         float dot = 0.f;
         const float* bv = a.xb_out ? a.xb_vec + (int64_t)a.xb_row[b] * a.xb_stride + head * 64 : nullptr;
+        const bool jit = a.jit_sigma != 0.f;
+        const uint32_t jrow = jit ? (uint32_t)((int64_t)a.jit_seq[b] * T + my_o) : 0u;
+        const uint32_t jdraw = jit ? (uint32_t)(a.jit_draw0 + b / a.jit_n_seq) : 0u;
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int d = dt * 32 + g * 8 + half * 4;
+            float jz[4] = {0.f, 0.f, 0.f, 0.f};
+            if (jit) {
+              dust_noise_quad(a.jit_seed, jdraw, a.jit_site, jrow, (uint32_t)(a.heads * 16), (uint32_t)((head * 64 + d) / 4),
+                              jz);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) jz[j] *= a.jit_sigma;
+            }
             bf16_t e[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              e[j] = f32_to_bf16(o_acc[og][dt][g * 4 + j] * inv);
+              e[j] = f32_to_bf16(o_acc[og][dt][g * 4 + j] * inv + jz[j]);
               if (bv) dot += bf16_to_f32(e[j]) * bv[d + j];
             }
             *(u32x2*)(og_ptr + d) = u32x2{(uint32_t)e[0] | ((uint32_t)e[1] << 16), (uint32_t)e[2] | ((uint32_t)e[3] << 16)};

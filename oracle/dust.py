@@ -1,6 +1,8 @@
 """ORACLE — test infrastructure only. Nothing in the product path may import or call this module.
 
-CPU restatement of Dust's head-slab CE estimator, DUST.head_error (train/val/dust.py:261-303), in fp32 torch, with
+CPU restatements, in fp32 torch, of Dust's direct draws (train/val/dust.py:195-259: the clean capture, rerun with
+block_forward's jitter sites (:104-120) and head_loss (:94-99), direct_errors with reward_to_go (:86-91)) and of its
+head-slab CE estimator, DUST.head_error (train/val/dust.py:261-303), with
 this build's counter-based jitter (oracle/rng.py head_noise) in place of the estimator's torch.randn draws
 (dust.py:192-193, 281). Chunks of n = chunk_size(draws, nrep) draws (dust.py:81-83) each jitter one 256-column
 slab of the cached lm_head outputs, in turn; a draw's loss is recomputed from the cached exponential sums of the
@@ -9,12 +11,18 @@ error of the slab's columns accumulates -(reward / sigma) * jitter, and the resu
 
 Pinned (tests/test_oracle_dust.py): the slab bookkeeping against a dense log-sum-exp of the jittered row, and, by
 Stein's lemma, the estimate over many small-sigma draws against (1 - 1/b) times the analytic gradient of the
-soft-capped CE with respect to the raw logits.
+soft-capped CE with respect to the raw logits. The direct draws: a rerun without jitter equals the clean per-token
+losses from every entry; reward_to_go against a brute-force double loop; by Stein's lemma, direct_errors over many
+draws against (1 - 1/n) times the autograd derivative of each token's loss with respect to that token's site
+activation (and, with gamma, the decayed sum over later tokens' losses).
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
+from oracle import model as om
 from oracle import rng
 
 SLAB = 256
@@ -73,3 +81,127 @@ def soft_capped_ce(raw, y, vocab=None):
     z = 15 * torch.tanh(raw[..., :vocab].float() / 15)
     ce = torch.logsumexp(z, -1) - z.gather(-1, y.clamp(min=0).unsqueeze(-1)).squeeze(-1)
     return torch.where(y != -1, ce, torch.zeros(()))
+
+
+# ---- the direct draws ---------------------------------------------------------------------------------------------
+
+SITE_ID = {'transformer.wte': 0, 'o': 1, 'attn': 2, 'fc': 3, 'mlp': 4}
+
+
+def parse_site(cfg, name):
+    """(block or None, site key, width): 'transformer.wte', 'o@{i}', or transformer.h.{i}.(attn.c_proj|mlp.c_fc|
+    mlp.c_proj)."""
+    if name == 'transformer.wte':
+        return None, 'transformer.wte', cfg.n_embd
+    if name.startswith('o@'):
+        return int(name[2:]), 'o', cfg.n_embd
+    parts = name.split('.')
+    key = {'attn.c_proj': 'attn', 'mlp.c_fc': 'fc', 'mlp.c_proj': 'mlp'}['.'.join(parts[3:])]
+    return int(parts[2]), key, 4 * cfg.n_embd if key == 'fc' else cfg.n_embd
+
+
+def dust_jitter(seed, draw, site, b, t, width):
+    """float32 [b, t, width]: one draw's jitter at one site, token rows b * t + t' (row-major)."""
+    return torch.from_numpy(rng.dust_noise(seed, draw, SITE_ID[site], 0, b * t, width)).view(b, t, width)
+
+
+def block_forward(p, cfg, i, x, idx, cos, sin, jitter=None):
+    """Block i on its (mixed) input x with jitter added at o / attn / fc / mlp (dust.py:104-120)."""
+    jitter = jitter or {}
+    add = lambda v, key: v if key not in jitter else v + jitter[key]
+    B, T, _ = x.shape
+    H, D = cfg.n_head, cfg.head_dim
+    pre = f'transformer.h.{i}.'
+    h = om.rms_norm(x)
+    q = (h @ p[pre + 'attn.c_q.weight'].t()).view(B, T, H, D)
+    k = (h @ p[pre + 'attn.c_k.weight'].t()).view(B, T, H, D)
+    v = (h @ p[pre + 'attn.c_v.weight'].t()).view(B, T, H, D)
+    if om.has_ve(i, cfg.n_layer):
+        ve = p[f'value_embeds.{i}.weight'][idx].view(B, T, H, D)
+        gate = 2 * torch.sigmoid(h[..., :32] @ p[pre + 'attn.ve_gate.weight'].t())
+        v = v + gate.unsqueeze(-1) * ve
+    q, k = om.rms_norm(om.apply_rotary(q, cos, sin)), om.rms_norm(om.apply_rotary(k, cos, sin))
+    y = add(om.attention(q, k, v, om.window_sizes(cfg)[i]).reshape(B, T, -1), 'o')
+    x = x + add(y @ p[pre + 'attn.c_proj.weight'].t(), 'attn')
+    hidden = add(om.rms_norm(x) @ p[pre + 'mlp.c_fc.weight'].t(), 'fc')
+    return x + add(torch.relu(hidden).square() @ p[pre + 'mlp.c_proj.weight'].t(), 'mlp')
+
+
+def head_loss(p, cfg, x, targets):
+    """Final norm, head, soft cap and per-token CE (dust.py:94-99): float32 [B, T], 0 at ignored targets."""
+    logits = (om.rms_norm(x) @ p['lm_head.weight'].t())[..., :cfg.vocab_size]
+    return om.softcap_ce(logits, targets)
+
+
+def capture(p, cfg, idx, targets):
+    """The clean pass: (blocks, x0, per-token losses [B, T]), blocks[i] = block i's mixed input (dust.py:195-208)."""
+    B, T = idx.shape
+    cos, sin = om.rotary(T, cfg.head_dim)
+    x = x0 = om.rms_norm(p['transformer.wte.weight'][idx])
+    blocks = []
+    for i in range(cfg.n_layer):
+        x = p['resid_lambdas'][i] * x + p['x0_lambdas'][i] * x0
+        blocks.append(x)
+        x = block_forward(p, cfg, i, x, idx, cos, sin)
+    return blocks, x0, head_loss(p, cfg, x, targets)
+
+
+def rerun(p, cfg, state, n, entry, sites, sigma, seed, draw0):
+    """Per-token losses [n, B, T] of draws draw0 .. draw0 + n - 1 with jitter at `sites` of block entry (None: the
+    token embedding), rerunning blocks entry onward from the captured input (dust.py:210-233)."""
+    blocks, x0, idx, targets = state['blocks'], state['x0'], state['idx'], state['targets']
+    B, T = idx.shape
+    cos, sin = om.rotary(T, cfg.head_dim)
+    jit = {}
+    for name in sites:
+        blk, key, width = parse_site(cfg, name)
+        if blk != entry:
+            raise ValueError(f'site {name!r} is not in block {entry}')
+        jit[key] = sigma * torch.cat([dust_jitter(seed, draw0 + j, key, B, T, width) for j in range(n)])
+    idx_n, tg_n = idx.repeat(n, 1), targets.repeat(n, 1)
+    if entry is None:
+        embedding = p['transformer.wte.weight'][idx_n]
+        x = x0n = om.rms_norm(embedding + jit['transformer.wte'])
+    else:
+        x, x0n = blocks[entry].repeat(n, 1, 1), x0.repeat(n, 1, 1)
+    for i in range(entry or 0, cfg.n_layer):
+        if entry is None or i > entry:
+            x = p['resid_lambdas'][i] * x + p['x0_lambdas'][i] * x0n
+        x = block_forward(p, cfg, i, x, idx_n, cos, sin, jit if i == entry else None)
+    return head_loss(p, cfg, x, tg_n).view(n, B, T)
+
+
+def reward_to_go(reward, gamma):
+    """Each token credited with the rewards at it and after it, decayed by gamma per token (dust.py:86-91)."""
+    lags = math.ceil(math.log(1e-6) / math.log(gamma))
+    kernel = gamma ** torch.arange(lags, dtype=reward.dtype)
+    padded = torch.nn.functional.pad(reward.flatten(0, 1).unsqueeze(1), (0, lags - 1))
+    return torch.nn.functional.conv1d(padded, kernel.view(1, 1, -1)).view_as(reward)
+
+
+def direct_errors(p, cfg, state, sites, draws, sigma, entry=None, gamma=0.0, nrep=16, seed=0, draw0=0):
+    """{site: error [B, T, width]}: one-sided loss drops centered across each chunk of draws, times the jitter
+    (dust.py:235-259); chunk c uses draws draw0 + c n .. draw0 + c n + n - 1."""
+    B, T = state['idx'].shape
+    n = chunk_size(draws, nrep)
+    info = {s: parse_site(cfg, s) for s in sites}
+    errors = {s: torch.zeros(B, T, w) for s, (_, _, w) in info.items()}
+    for c in range(draws // n):
+        d0 = draw0 + c * n
+        loss = rerun(p, cfg, state, n, entry, sites, sigma, seed, d0)
+        for s, (_, key, width) in info.items():
+            errors[s] += chunk_errors(loss, state['clean'], sigma, gamma, seed, d0, key, width)
+    return {s: e / draws for s, e in errors.items()}
+
+
+def chunk_errors(loss, clean, sigma, gamma, seed, d0, key, width):
+    """One chunk's term of a site's error sum (dust.py:246-257): -(reward a) / sigma summed over the chunk's draws,
+    reward = clean - loss [n, B, T] centered over the draws, then its reward-to-go when gamma > 0."""
+    n, B, T = loss.shape
+    reward = clean.unsqueeze(0) - loss
+    if n > 1:
+        reward = reward - reward.mean(0, keepdim=True)
+    if gamma:
+        reward = reward_to_go(reward, gamma)
+    a = torch.stack([dust_jitter(seed, d0 + j, key, B, T, width) for j in range(n)])
+    return -torch.einsum('nbt,nbtd->btd', reward, a) / sigma

@@ -17,6 +17,9 @@
  *     off = (out0 * range) >> 32 with range = 2^28 - sum(shape), i.e. an integer in [0, range).
  *   head-slab jitter (the replacement of train/val/dust.py:281's torch.randn): value d < 256 of draw g at token
  *     row r = lane d & 3 of Box-Muller on philox(ctr = (64 r + d / 4, g, 0, STREAM_HEAD), key = (seed_lo, seed_hi)).
+ *   direct-draw jitter (the replacement of train/val/dust.py:244's torch.randn): channel d of a site `width` wide,
+ *     draw g, site s, token row r = lane d & 3 of Box-Muller on philox(ctr = (r width / 4 + d / 4, g, s, STREAM_DUST),
+ *     key = (seed_lo, seed_hi)).
  * Box-Muller: u1 = ((x >> 8) + 1) * 2^-24 in (0, 1], u2 = (y >> 8) * 2^-24 in [0, 1);
  *   r = sqrt(-2 ln u1), z0 = r cos(2 pi u2), z1 = r sin(2 pi u2).
  * ln, sin and cos are this file's own polynomials (atanh series for ln, Taylor series for sin/cos on [-pi/4, pi/4)
@@ -37,6 +40,7 @@
 #define STREAM_BUFFER 0x4E4F4953u /* "NOIS" */
 #define STREAM_OFFSET 0x4F464653u /* "OFFS" */
 #define STREAM_HEAD 0x44414548u   /* "HEAD" */
+#define STREAM_DUST 0x54535544u   /* "DUST" */
 
 void oracle_philox4x32_10(const uint32_t ctr_in[4], const uint32_t key_in[2], uint32_t out[4]) {
     uint32_t c0 = ctr_in[0], c1 = ctr_in[1], c2 = ctr_in[2], c3 = ctr_in[3];
@@ -165,6 +169,22 @@ void oracle_head_noise(uint64_t seed, uint32_t draw, uint32_t row0, int64_t n, f
             uint32_t ctr[4] = {((uint32_t)row0 + (uint32_t)i) * 64u + q, draw, 0u, STREAM_HEAD};
             uint32_t r[4];
             float* z = out + i * 256 + 4 * q;
+            oracle_philox4x32_10(ctr, key, r);
+            oracle_box_muller(r[0], r[1], &z[0], &z[1]);
+            oracle_box_muller(r[2], r[3], &z[2], &z[3]);
+        }
+}
+
+/* out[i, d] = direct-draw jitter of draw `draw` at site `site`, token rows row0 + i (i < n), d < width (% 4 == 0). */
+void oracle_dust_noise(uint64_t seed, uint32_t draw, uint32_t site, uint32_t row0, int64_t n, int32_t width,
+                       float* out) {
+    uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    const uint32_t quads = (uint32_t)width / 4u;
+    for (int64_t i = 0; i < n; ++i)
+        for (uint32_t q = 0; q < quads; ++q) {
+            uint32_t ctr[4] = {((uint32_t)row0 + (uint32_t)i) * quads + q, draw, site, STREAM_DUST};
+            uint32_t r[4];
+            float* z = out + i * width + 4 * q;
             oracle_philox4x32_10(ctr, key, r);
             oracle_box_muller(r[0], r[1], &z[0], &z[1]);
             oracle_box_muller(r[2], r[3], &z[2], &z[3]);

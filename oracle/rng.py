@@ -38,6 +38,8 @@ def lib():
                                            ctypes.c_void_p]
         _lib.oracle_head_noise.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int64,
                                            ctypes.c_void_p]
+        _lib.oracle_dust_noise.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                           ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
     return _lib
 
 
@@ -101,4 +103,11 @@ def head_noise(seed, draw, row0, n):
     """float32 [n, 256]: the head-slab estimator's jitter of one draw at token rows row0 .. row0 + n - 1."""
     out = np.empty((n, 256), np.float32)
     lib().oracle_head_noise(seed, draw, row0, n, out.ctypes.data)
+    return out
+
+
+def dust_noise(seed, draw, site, row0, n, width):
+    """float32 [n, width]: the direct draws' jitter of one draw at one site, token rows row0 .. row0 + n - 1."""
+    out = np.empty((n, width), np.float32)
+    lib().oracle_dust_noise(seed, draw, site, row0, n, width, out.ctypes.data)
     return out

@@ -44,3 +44,91 @@ def test_head_error_rejects_uneven_slabs(dev):
     raw, y, clean = _case(1, 16, 512, seed=1)
     with pytest.raises(ValueError):  # one chunk of 16 draws cannot cover 2 slabs
         dust.head_error(raw.to(dev), y.to(dev), clean.to(dev), 16, nrep=16)
+
+
+# ---- the direct draws: capture, rerun and error sums (noise_dust_capture / _rerun / _errors; dust.py:195-259) ------
+
+from oracle import model as om
+from tests.golden import recipe
+
+SEQ = 256
+_ST = {}
+
+
+def _setup(dev):
+    if 'st' not in _ST:
+        from tests.test_gpu_forward import _model
+        from noise_amd.model import GPTConfig
+        ocfg = om.Config(sequence_len=SEQ)
+        w = recipe.weights(ocfg, seed=99)
+        idx, tg = recipe.tokens(ocfg, batch=2, ignore_every=37)
+        blocks, x0, clean = od.capture(w, ocfg, idx, tg)
+        _ST['st'] = (ocfg, w, dict(blocks=blocks, x0=x0, idx=idx, targets=tg, clean=clean),
+                     _model(dev, w, GPTConfig(sequence_len=SEQ)))
+    return _ST['st']
+
+
+def test_capture_matches_oracle(dev):
+    print('dust capture B=2 T=256', flush=True)
+    from noise_amd.dust import Dust
+    ocfg, w, st, model = _setup(dev)
+    d = Dust(model)
+    clean = d.capture(st['idx'].to(dev), st['targets'].to(dev)).cpu()
+    mask = st['targets'] >= 0
+    assert ((clean - st['clean']).abs()[mask] / st['clean'][mask].abs()).max().item() < 1e-2
+    assert torch.all(clean[~mask] == 0)
+    for i in range(ocfg.n_layer):
+        got, ref = d.blocks[i].cpu(), st['blocks'][i]
+        assert ((got - ref).norm() / ref.norm()).item() < 1e-2, i
+    assert ((d.x0.cpu() - st['x0']).norm() / st['x0'].norm()).item() < 1e-3
+
+
+@pytest.mark.parametrize('entry,sites', [
+    (None, ['transformer.wte']),
+    (0, ['o@0']),
+    (1, ['transformer.h.1.attn.c_proj', 'transformer.h.1.mlp.c_proj']),  # the writers, jittered together
+    (5, ['transformer.h.5.mlp.c_fc']),
+    (7, ['transformer.h.7.mlp.c_proj']),
+])
+def test_rerun_matches_oracle(dev, entry, sites):
+    print(f'dust rerun entry={entry} sites={sites}', flush=True)
+    from noise_amd.dust import Dust
+    ocfg, w, st, model = _setup(dev)
+    d = Dust(model, seed=5)
+    d.capture(st['idx'].to(dev), st['targets'].to(dev))
+    got = d.rerun(3, entry, sites, 0.4, draw0=7).cpu()
+    ref = od.rerun(w, ocfg, st, 3, entry, sites, 0.4, seed=d.seed, draw0=7)
+    mask = (st['targets'] >= 0).expand(3, -1, -1)
+    assert ((got - ref).abs()[mask] / ref[mask].abs()).max().item() < 1e-2
+    assert (got - st['clean'].to(got)).abs().max() > 1e-3  # the jitter moved the losses
+
+
+@pytest.mark.parametrize('gamma', [0.0, 0.3])
+def test_error_sums_match_oracle_on_the_same_losses(dev, gamma):
+    """The reward and error kernels against oracle/dust.py chunk_errors on the GPU's own per-token losses (1e-4 of the
+    largest |error|: the same fp32 arithmetic in another order); then direct_errors equals its chunks' sum."""
+    print(f'dust error sums gamma={gamma}', flush=True)
+    from noise_amd import _lib
+    from noise_amd.dust import Dust
+    ocfg, w, st, model = _setup(dev)
+    d = Dust(model, nrep=4, seed=2)
+    d.capture(st['idx'].to(dev), st['targets'].to(dev))
+    sites, entry, sigma = ['transformer.h.2.mlp.c_fc', 'transformer.h.2.attn.c_proj'], 2, 0.4
+    chunks = []
+    for d0 in (0, 4):
+        loss = d.rerun(4, entry, sites, sigma, draw0=d0)
+        chunks.append(loss.cpu())
+        for name, key, width in [(sites[0], 'fc', 2048), (sites[1], 'attn', 512)]:
+            err = torch.zeros(2, SEQ, width, device=dev)
+            ws = torch.empty(_lib.lib().noise_dust_errors_workspace(4, 2, SEQ), dtype=torch.uint8, device=dev)
+            _lib.call('noise_dust_errors', _lib.ptr(loss), _lib.ptr(d.clean_loss), 4, 2, SEQ, gamma, sigma, d.seed, d0,
+                      od.SITE_ID[key], width, _lib.ptr(err), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+            ref = od.chunk_errors(loss.cpu(), d.clean_loss.cpu(), sigma, gamma, d.seed, d0, key, width)
+            assert (((err.cpu() - ref).abs().max()) / ref.abs().max()).item() < 1e-4, (name, d0)
+    d.next_draw = 0
+    est = d.direct_errors(sites, 8, sigma, entry=entry, gamma=gamma)
+    for name, key, width in [(sites[0], 'fc', 2048), (sites[1], 'attn', 512)]:
+        ref = sum(od.chunk_errors(c, d.clean_loss.cpu(), sigma, gamma, d.seed, d0, key, width)
+                  for c, d0 in zip(chunks, (0, 4))) / 8
+        assert (((est[name].cpu() - ref).abs().max()) / ref.abs().max()).item() < 1e-4, name
+    assert d.next_draw == 8

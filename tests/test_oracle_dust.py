@@ -79,3 +79,72 @@ def test_chunks_must_cover_slabs():
     y = torch.zeros(1, 1, dtype=torch.long)
     with pytest.raises(ValueError):
         od.head_error(raw, y, od.soft_capped_ce(raw, y), draws=16, nrep=16)  # 1 chunk, 2 slabs
+
+
+# ---- the direct draws (oracle/dust.py capture / rerun / direct_errors, dust.py:195-259) ---------------------------
+
+from oracle import model as om
+from tests.golden import recipe
+
+
+def _small_state(B=2):
+    cfg = om.Config(**recipe.SMALL)
+    p = recipe.weights(cfg)
+    idx, tg = recipe.tokens(cfg, batch=B, ignore_every=11)
+    blocks, x0, clean = od.capture(p, cfg, idx, tg)
+    return cfg, p, dict(blocks=blocks, x0=x0, idx=idx, targets=tg, clean=clean)
+
+
+def test_capture_matches_forward_and_rerun_without_jitter_is_clean():
+    cfg, p, st = _small_state()
+    ref = om.gpt_forward(p, cfg, st['idx'], st['targets'], 'none').view_as(st['clean'])
+    assert torch.allclose(st['clean'], ref, rtol=1e-5, atol=1e-6)
+    for entry, sites in [(None, ['transformer.wte']), (0, ['o@0']), (1, ['transformer.h.1.mlp.c_fc']),
+                         (3, ['transformer.h.3.attn.c_proj', 'transformer.h.3.mlp.c_proj'])]:
+        loss = od.rerun(p, cfg, st, 3, entry, sites, 0.0, seed=1, draw0=0)
+        assert torch.equal(loss, st['clean'].expand(3, -1, -1)), entry
+
+
+def test_reward_to_go_is_the_decayed_future_sum():
+    g = torch.Generator().manual_seed(4)
+    r = torch.randn(3, 2, 40, generator=g, dtype=torch.float64)
+    gamma = 0.3
+    lags = math.ceil(math.log(1e-6) / math.log(gamma))
+    got = od.reward_to_go(r, gamma)
+    ref = torch.zeros_like(r)
+    for t in range(40):
+        for k in range(lags):
+            if t + k < 40:
+                ref[..., t] += gamma ** k * r[..., t + k]
+    assert torch.allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def _own_token_grad(p, cfg, st, entry, key, width):
+    """d loss[b, t] / d site[b, t, :] by autograd on the oracle's block forward (jitter leaf at zero)."""
+    idx, tg = st['idx'], st['targets']
+    B, T = idx.shape
+    cos, sin = om.rotary(T, cfg.head_dim)
+    z = torch.zeros(B, T, width, requires_grad=True)
+    x = st['blocks'][entry]
+    for i in range(entry, cfg.n_layer):
+        if i > entry:
+            x = p['resid_lambdas'][i] * x + p['x0_lambdas'][i] * st['x0']
+        x = od.block_forward(p, cfg, i, x, idx, cos, sin, {key: z} if i == entry else None)
+    loss = od.head_loss(p, cfg, x, tg)
+    g = torch.zeros(B, T, width)
+    for b in range(B):
+        for t in range(T):
+            if tg[b, t] >= 0:
+                g[b, t] = torch.autograd.grad(loss[b, t], z, retain_graph=True)[0][b, t]
+    return g
+
+
+def test_direct_errors_tend_to_scaled_own_token_gradient():
+    """Stein's lemma: E[-(reward / sigma) a] -> (1 - 1/n) d loss_t / d site_t for small sigma; chunks of n = 2 make the
+    centering's factor 1/2, so a missing centering (factor 1) or a wrong sign or token pairing fails."""
+    cfg, p, st = _small_state()
+    site, entry = 'o@2', 2
+    g = _own_token_grad(p, cfg, st, entry, 'o', cfg.n_embd)
+    est = od.direct_errors(p, cfg, st, [site], draws=3072, sigma=0.02, entry=entry, nrep=2, seed=3)[site]
+    slope = (est * g).sum() / (g * g).sum()
+    assert 0.4 < slope.item() < 0.6, slope.item()
