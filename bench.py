@@ -12,7 +12,8 @@ A step is one pass of the hot path over one batch of synthetic input:
       512 members, fitness, outer-product gradient assembly and AdamW. 50,331,648 member-tokens.
 The JSON line carries the metric of BASELINE.json, the roofline of the dominant kernel (HIP events on the launch
 stream over the timed region), the oracle's CPU throughput on a bounded sample, the credit readout's TFLOP/s at
-config 3 (B16 H8 T2048 d64), and the time of Dust's head-slab estimator at the reference recipe's per-GPU draws. `roofline.traffic` is the dominant kernel's HBM bytes per launch as recorded in
+config 3 (B16 H8 T2048 d64), and the time of Dust's head-slab estimator and of one group of its direct draws at the
+reference recipe's per-GPU draw counts. `roofline.traffic` is the dominant kernel's HBM bytes per launch as recorded in
 profiles/population_forward_c4_traffic.txt (rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this script, each scaled
 by what the counter reads for --copy-calibration); it is null for a workload or kernel that file does not cover.
 """
@@ -284,6 +285,35 @@ def bench_head_error(dev, iters=3):
                      'twice from the counter stream (loss, then error), never stored')
 
 
+def bench_dust_direct(dev, model, iters=2):
+    """Dust's direct draws (train/val/dust.py:195-259) at the reference recipe's per-GPU counts: one direct_errors
+    call for block 0's writers (attn.c_proj and mlp.c_proj outputs jittered together; recipe(1.5).writers = 384 draws
+    over 8 GPUs = 48, chunks of nrep 16) on the 8 x 2048 batch; every draw reruns all 8 blocks."""
+    import torch
+    from noise_amd import _lib
+    from noise_amd.dust import Dust
+    x, y = zipf_tokens(8, T_SEQ, seed=1)
+    x, y = x.to(dev), y.to(dev)
+    d = Dust(model, nrep=16)
+    d.capture(x, y)
+    sites = ['transformer.h.0.attn.c_proj', 'transformer.h.0.mlp.c_proj']
+    d.direct_errors(sites, 16, 0.4, entry=0)
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        err = d.direct_errors(sites, 48, 0.4, entry=0)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / iters
+    tm = _lib.timing_read()
+    _lib.timing_enable(False)
+    member_tokens = 48 * 8 * T_SEQ
+    return dict(ms=round(dt * 1e3, 2), draws=48, sequences=8, seq_len=T_SEQ,
+                rerun_ms=round(tm['dust_rerun'][1] / iters, 2), errors_ms=round(tm['dust_errors'][1] / iters, 2),
+                rerun_member_tokens_per_s=round(member_tokens / (tm['dust_rerun'][1] / iters * 1e-3), 1),
+                finite=all(bool(torch.isfinite(e).all()) for e in err.values()))
+
+
 def cpu_baseline(model, sample_members=4, T=T_SEQ, reps=3):
     """The oracle (fp32 eager torch on the host cores) on a bounded sample of the same population forward."""
     import torch
@@ -358,6 +388,7 @@ def main():
         line['credit'] = bench_credit(dev)
     if not args.no_dust:
         line['dust_head_error'] = bench_head_error(dev)
+        line['dust_direct'] = bench_dust_direct(dev, model)
     if not args.no_cpu_baseline:
         line['cpu_baseline'] = cpu_baseline(model)
     print(json.dumps(line), flush=True)
