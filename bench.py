@@ -185,13 +185,28 @@ def bench_c5(args, dev):
     x, y = x.to(dev), y.to(dev)
     es = Eggroll(model, pairs, sigma=0.002, seed=0, chunk=256)
     opt = AdamW(model.parameters(), lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    # the step's credit readout over the clean batch (B 8, 8 heads, 8 layers, T window): per-token error signals of
+    # dim 64 credited through each layer's q / k (synthetic, as config 3's)
+    from noise_amd import credit
+    g = torch.Generator(device=dev).manual_seed(1)
+    cq = (torch.randn(n_seq * 8, T_SEQ, 64, device=dev, generator=g) / 8).bfloat16()
+    ck = (torch.randn(n_seq * 8, T_SEQ, 64, device=dev, generator=g) / 8).bfloat16()
+    ce = torch.randn(n_seq * 8, T_SEQ, 64, device=dev, generator=g)
+    n_layer = model.config.n_layer
+
+    def step(i):
+        loss = es.step(x, y, opt, i)
+        for _ in range(n_layer):
+            credit.value_credit(cq, ck, ce, T_SEQ)
+        return loss
+
     for i in range(args.warmup):
-        es.step(x, y, opt, i + 1)
+        step(i + 1)
     torch.cuda.synchronize()
     _lib.timing_enable(True)
     t0 = time.perf_counter()
     for i in range(args.steps):
-        loss = es.step(x, y, opt, args.warmup + i + 1)
+        loss = step(args.warmup + i + 1)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     timing = _lib.timing_read()
@@ -203,7 +218,8 @@ def bench_c5(args, dev):
     res = dict(value=member_tokens * args.steps / dt, ms_per_step=dt / args.steps * 1e3, member_tokens=member_tokens,
                roofline=roof, kernels=kernels, finite=math.isfinite(loss), mean_member_ce=loss,
                config=dict(workload='C5: full EGGROLL step, 24,576 members (12,288 pairs) in chunks of 512 over an '
-                           '8 x 2048 Zipf(1.1) batch, fitness, outer-product gradients, AdamW',
+                           '8 x 2048 Zipf(1.1) batch, fitness, outer-product gradients, AdamW, and the credit readout '
+                           'over the clean batch (8 layers x B8 H8 T2048, synthetic q / k / error signals)',
                            members=members, seq_len=T_SEQ, n_layer=len(windows), parallelism='single GPU'))
     res['model'] = model
     return res
@@ -314,7 +330,7 @@ def bench_dust_direct(dev, model, iters=2):
                 finite=all(bool(torch.isfinite(e).all()) for e in err.values()))
 
 
-def cpu_baseline(model, sample_members=4, T=T_SEQ, reps=3):
+def cpu_baseline(model, sample_members=8, T=T_SEQ, reps=3):
     """The oracle (fp32 eager torch on the host cores) on a bounded sample of the same population forward."""
     import torch
     from oracle import eggroll as oe
