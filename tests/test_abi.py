@@ -88,3 +88,42 @@ def test_eggroll_member_layout_matches_oracle():
     rd, rs, rq = member_layout(12288, 8)
     assert members == 24576
     assert np.array_equal(d.numpy(), rd) and np.array_equal(s.numpy(), rs) and np.array_equal(q.numpy(), rq)
+
+
+def test_dust_and_head_error_arguments_are_checked_before_any_gpu_call():
+    from noise_amd import _lib
+    p = ctypes.c_void_p(16)
+    # head-slab estimator (dust.py:261-303): vocabulary in 256-column slabs, chunks covering the slabs evenly
+    with pytest.raises(ValueError, match='multiple of 256'):
+        _lib.call('noise_head_error', p, 300, p, p, 1, 4, 300, 16, 16, 0.1, 0, p, p, 1 << 30, None)
+    with pytest.raises(ValueError, match='slabs evenly'):
+        _lib.call('noise_head_error', p, 512, p, p, 1, 4, 512, 16, 16, 0.1, 0, p, p, 1 << 30, None)
+    with pytest.raises(ValueError, match='65,535'):
+        _lib.call('noise_head_error', p, 256, p, p, 1, 4, 256, 70000, 16, 0.1, 0, p, p, 1 << 40, None)
+    with pytest.raises(ValueError, match='workspace'):
+        _lib.call('noise_head_error', p, 256, p, p, 1, 4, 256, 16, 16, 0.1, 0, p, p, 8, None)
+    assert _lib.lib().noise_head_error_workspace(8, 512, 16) >= 16 * 8 * 4
+    # direct draws' error sums (dust.py:235-259)
+    with pytest.raises(ValueError, match='sigma'):
+        _lib.call('noise_dust_errors', p, p, 4, 2, 128, 0.0, 0.0, 0, 0, 3, 2048, p, p, 1 << 30, None)
+    with pytest.raises(ValueError, match='gamma'):
+        _lib.call('noise_dust_errors', p, p, 4, 2, 128, 1.0, 0.4, 0, 0, 3, 2048, p, p, 1 << 30, None)
+    with pytest.raises(ValueError, match='site'):
+        _lib.call('noise_dust_errors', p, p, 4, 2, 128, 0.0, 0.4, 0, 0, 5, 512, p, p, 1 << 30, None)
+    with pytest.raises(ValueError, match='workspace'):
+        _lib.call('noise_dust_errors', p, p, 4, 2, 128, 0.0, 0.4, 0, 0, 3, 2048, p, p, 8, None)
+    assert _lib.lib().noise_dust_errors_workspace(4, 2, 128) >= 2 * 4 * 2 * 128 * 4
+    assert _lib.lib().noise_dust_workspace(0, 2, 128) == 0
+    # reruns (dust.py:210-233): the entry, its sites and its captured input
+    model = _lib.NoiseGpt()
+    model.n_layer = 8
+    d = _lib.NoiseDustDraws()
+    d.entry, d.sites, d.sigma, d.n_draws = 8, 2, 0.4, 4
+    with pytest.raises(ValueError, match='entry'):
+        _lib.call('noise_dust_rerun', ctypes.byref(model), ctypes.byref(d), p, p, 2, 128, p, p, 1 << 30, None)
+    d.entry, d.sites = 3, 1  # the embedding's site on a block
+    with pytest.raises(ValueError, match='do not belong'):
+        _lib.call('noise_dust_rerun', ctypes.byref(model), ctypes.byref(d), p, p, 2, 128, p, p, 1 << 30, None)
+    d.sites = 4  # a block site without the captured input
+    with pytest.raises(ValueError, match='captured input'):
+        _lib.call('noise_dust_rerun', ctypes.byref(model), ctypes.byref(d), p, p, 2, 128, p, p, 1 << 30, None)
