@@ -77,8 +77,13 @@ struct FlashStage<kCredit> {
   float lse;
 };
 
+// Bounded attention (the model's forward) fits 128 VGPRs, so four workgroups share a CU (4 x 32 KB of LDS); the other
+// modes need more registers and keep two.
+template <int MODE, bool BOUNDED>
+constexpr int kFlashOccupancy = (MODE == kAttn && BOUNDED) ? 4 : 2;
+
 template <int MODE, bool BOUNDED, int OG>
-__global__ __launch_bounds__(256, 2) void window_flash_kernel(FlashArgs a) {
+__global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_flash_kernel(FlashArgs a) {
   constexpr int kBO = FlashTile<OG>::BO;
   __shared__ __align__(16) bf16_t ys[2][64 * 64];
   __shared__ __align__(16) bf16_t vt_hi[2][64 * 64];
