@@ -15,9 +15,10 @@
 // y from LDS as the A operand, x in registers as the B operand): the accumulator layout of S^T (lane = output l%32,
 // registers = 16 inputs) is exactly the B-operand layout of O^T[d, o] += V^T[d, i] P^T[i, o], so probabilities go
 // from score registers to the value MFMA without an LDS round trip. Every y and V fragment read from LDS feeds all
-// output groups of a wave. Values are staged row-major like y (16-byte chunks XOR-swizzled by row, so a half-wave's
-// reads hit distinct banks; kCredit's fp32 source as bf16 high and low parts), and the V^T operand fragments are
-// read with gfx950's transposing LDS read (ds_read_b64_tr_b16).
+// output groups of a wave. y is staged row-major in 16-byte chunks XOR-swizzled by row pairs, so a quarter-wave's
+// row reads hit distinct banks. Values are staged row-major too, kAttn's and kCenter's like y, kCredit's fp32 source
+// as bf16 high and, on request, low parts in 8-byte units swizzled for the transposing LDS read (ds_read_b64_tr_b16,
+// vt_slot) that builds the V^T operand fragments.
 //
 // kCenter computes the value scores the same way as the logits, S2^T[i, o] = v_i . hub_o (v staged in LDS like y,
 // hub in registers like x), and accumulates sum_i p_i s2_i beside sum_i p_i with fp32 probabilities.
@@ -60,6 +61,12 @@ struct FlashArgs {
 };
 
 constexpr int kFlashBI = 64;
+
+// LDS element index of 8-byte unit u (channels 4u .. 4u+3) of value row r in the layout read by ds_read_b64_tr_b16.
+// One such read has each half-wave take 8 units of 4 consecutive rows; slot u ^ 4 (r & 3) puts those 32 pieces on
+// 64 distinct banks (64 banks of 4 bytes; rows of 128 bytes alternate between the two bank halves). A 16-byte chunk
+// (units 2c, 2c+1) stays contiguous, so row stores by 8 or 16 bytes are conflict-free as well.
+__device__ __forceinline__ int vt_slot(int r, int u) { return r * 64 + ((u ^ ((r & 3) << 2)) << 2); }
 template <int OG> struct FlashTile { static constexpr int BO = 4 * 32 * OG; };  // outputs per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -77,10 +84,11 @@ struct FlashStage<kCredit> {
   float lse;
 };
 
-// Bounded attention (the model's forward) fits 128 VGPRs, so four workgroups share a CU (4 x 32 KB of LDS); the other
+// Waves per SIMD the registers are sized for. Bounded attention (the model's forward) fits 128 VGPRs, so four
+// workgroups share a CU (4 x 32 KB of LDS); the credit value pass fits 168 (three workgroups, 3 x 48.5 KB); the other
 // modes need more registers and keep two.
 template <int MODE, bool BOUNDED>
-constexpr int kFlashOccupancy = (MODE == kAttn && BOUNDED) ? 4 : 2;
+constexpr int kFlashOccupancy = (MODE == kAttn && BOUNDED) ? 4 : (MODE == kCredit ? 3 : 2);
 
 template <int MODE, bool BOUNDED, int OG>
 __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_flash_kernel(FlashArgs a) {
@@ -221,13 +229,13 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
           const float f0 = st.v[k][2 * j], f1 = st.v[k][2 * j + 1];
           const bf16_t h0 = f32_to_bf16(f0), h1 = f32_to_bf16(f1);
           hi[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-          lo[j] = pack_bf16x2(f0 - bf16_to_f32(h0), f1 - bf16_to_f32(h1));
+          if (a.hi_lo) lo[j] = pack_bf16x2(f0 - bf16_to_f32(h0), f1 - bf16_to_f32(h1));
         }
-        const int at = row * 64 + (((c4 >> 1) ^ ((row >> 1) & 7)) * 8) + (c4 & 1) * 4;
+        const int at = vt_slot(row, c4);
         *(u32x2*)(&vt_hi[s][at]) = u32x2{hi[0], hi[1]};
-        *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0], lo[1]};
+        if (a.hi_lo) *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0], lo[1]};
       }
-      if (tid < 64) lse_s[s][tid] = st.lse;
+      if (tid < 64) lse_s[s][tid] = st.lse * kLog2e;  // staged in log2 units
     } else if constexpr (MODE == kCenter || MODE == kAttn) {
 #pragma unroll
       for (int rep = 0; rep < 2; ++rep) {
@@ -323,7 +331,7 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int il = t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-              sc[og][t][r] = fast_exp2(sc[og][t][r] * qk_scale - lse_s[s][il] * kLog2e);
+              sc[og][t][r] = fast_exp2(fmaf(sc[og][t][r], qk_scale, -lse_s[s][il]));
             }
         } else if (bounded) {
           float ls = 0.f;
@@ -337,16 +345,14 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
             }
           l_run[og] += ls;
         } else {
+          // the maximum of the raw scores, scaled once (the scale is positive and rounding is monotonic, so this is
+          // the maximum of the scaled scores); each weight is then one fma and one exp2
           float mt = -INFINITY;
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float e = sc[og][t][r] * qk_scale;
-              sc[og][t][r] = e;
-              mt = fmaxf(mt, e);
-            }
-          mt = fmaxf(mt, lane_xor32(mt, lane));
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[og][t][r]);
+          mt = fmaxf(mt, lane_xor32(mt, lane)) * qk_scale;
           const float m_new = fmaxf(m_run[og], mt);
           const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
           const float corr = fast_exp2(m_run[og] - m_safe);
@@ -355,7 +361,7 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const float p = fast_exp2(sc[og][t][r] - m_safe);
+              const float p = fast_exp2(fmaf(sc[og][t][r], qk_scale, -m_safe));
               sc[og][t][r] = p;
               ls += p;
               if constexpr (MODE == kCenter) cs = fmaf(p, s2[og][t][r], cs);
@@ -392,8 +398,12 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
               const int grp = lane >> 4;
               const int d0 = dt * 32 + 16 * (grp & 1) + 4 * (lane & 3);
               const int i_a = base + 4 * (grp >> 1) + ((lane >> 2) & 3), i_b = i_a + 8;
-              const int at_a = i_a * 64 + (((d0 >> 3) ^ ((i_a >> 1) & 7)) * 8) + (d0 & 7);
-              const int at_b = i_b * 64 + (((d0 >> 3) ^ ((i_b >> 1) & 7)) * 8) + (d0 & 7);
+              // kCredit: the conflict-free layout of vt_slot. kAttn keeps y's row layout (2-way bank conflicts on these
+              // reads): vt_slot's addressing takes it past 128 VGPRs, and it measured no faster at equal occupancy.
+              const int at_a = (MODE == kCredit) ? vt_slot(i_a, d0 >> 2)
+                                                 : i_a * 64 + (((d0 >> 3) ^ ((i_a >> 1) & 7)) * 8) + (d0 & 7);
+              const int at_b = (MODE == kCredit) ? vt_slot(i_b, d0 >> 2)
+                                                 : i_b * 64 + (((d0 >> 3) ^ ((i_b >> 1) & 7)) * 8) + (d0 & 7);
               const v4s ra = ds_read_tr16(&vt_hi[s][at_a]), rb = ds_read_tr16(&vt_hi[s][at_b]);
               const bf16x8 vf = __builtin_bit_cast(bf16x8, s16x8{ra[0], ra[1], ra[2], ra[3], rb[0], rb[1], rb[2], rb[3]});
 #pragma unroll
