@@ -100,13 +100,20 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
 
   const int T = a.T, W = a.window;
   const int n_tiles = (T + kBO - 1) / kBO;
-  // Workgroups go round-robin to the 8 XCDs. When the (batch, head) rows divide by 8, XCD x takes rows x, x + 8, ...
-  // and runs every output tile of a row back to back, so the row's inputs (512 KB at T = 2048) stay in its L2.
+  // Workgroup order. When every row's inputs together fit well inside the 256 MB Infinity Cache, the tiles are
+  // dispatched heaviest first across all rows (tile rank outer, rows inner): a launch of a few rounds of workgroups
+  // then ends on its lightest tiles instead of on a late heavy one. Otherwise workgroups go round-robin to the 8 XCDs
+  // and, when the (batch, head) rows divide by 8, XCD x takes rows x, x + 8, ... and runs every output tile of a row
+  // back to back, so the row's inputs (512 KB at T = 2048) stay in its L2.
   const int64_t n_rows = (int64_t)gridDim.y * gridDim.z;
   const int64_t bid = blockIdx.x + (int64_t)n_tiles * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  constexpr int64_t kInBytes = 128 + (MODE == kCredit ? 256 : MODE == kLse ? 0 : 128);  // input bytes per token
   int64_t row_idx;
   int tile_idx;
-  if (n_rows % 8 == 0) {
+  if (n_rows * T * kInBytes <= (128ll << 20)) {
+    tile_idx = (int)(bid / n_rows);
+    row_idx = bid % n_rows;
+  } else if (n_rows % 8 == 0) {
     const int64_t slot = bid >> 3;
     row_idx = (bid & 7) + 8 * (slot / n_tiles);
     tile_idx = (int)(slot % n_tiles);
