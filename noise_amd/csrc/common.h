@@ -27,9 +27,12 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t v) { return __uint_as_float(
 // Round-to-nearest-even fp32 -> bf16, the rounding of torch's .to(torch.bfloat16) (gfx950 converts in hardware).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
-// Two floats as a bf16 pair (low half first), and back.
+// Two floats as a bf16 pair (low half first), and back. The pair converts as a 2-vector, one v_cvt_pk_bf16_f32
+// (round to nearest even per element, as f32_to_bf16) instead of two conversions, a shift and an or.
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_v{lo, hi}), bf16x2_v));
 }
 __device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }

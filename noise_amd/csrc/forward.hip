@@ -136,12 +136,13 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
   ss = warp_sum(ss);
   const float inv = rsqrtf(ss * (1.0f / kD) + kNormEps);
   float hv[8];
-  bf16_t hb[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) { hb[j] = f32_to_bf16(v[j] * inv); hv[j] = bf16_to_f32(hb[j]); }
   u32x4 packed;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) packed[j] = (uint32_t)hb[2 * j] | ((uint32_t)hb[2 * j + 1] << 16);
+  for (int j = 0; j < 4; ++j) {
+    packed[j] = pack_bf16x2(v[2 * j] * inv, v[2 * j + 1] * inv);
+    hv[2 * j] = bf16_lo(packed[j]);
+    hv[2 * j + 1] = bf16_hi(packed[j]);
+  }
   *(u32x4*)(a.h + r * kD + c0) = packed;
   if (nr) {
     for (int k = 0; k < a.ndot; ++k) {
@@ -224,16 +225,7 @@ __global__ __launch_bounds__(256) void gate_kernel(Members mb, const bf16_t* __r
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; }
 
 __device__ __forceinline__ void st_bf16x4(bf16_t* p, f32x4 v) {
-  const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-  const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-  *(u32x2*)p = u32x2{lo, hi};
-}
-
-__device__ __forceinline__ f32x4 bf16_round4(f32x4 v) {
-  f32x4 r;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) r[k] = bf16_to_f32(f32_to_bf16(v[k]));
-  return r;
+  *(u32x2*)p = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 
 // q|k|v = h W_qkv^T + s (h . b_seg) a_seg (eggroll.py:80-84); on q and k columns then the rotary embedding and the
@@ -460,10 +452,10 @@ struct EpiResidNorm {
       for (int k = 0; k < kNDot; ++k) dk[k][q] = 0.f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        f32x4 hv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) hv[e] = bf16_to_f32(f32_to_bf16(v[q][hh][e] * inv));
-        st_bf16x4(h + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane, hv);
+        const uint32_t p0 = pack_bf16x2(v[q][hh][0] * inv, v[q][hh][1] * inv);
+        const uint32_t p1 = pack_bf16x2(v[q][hh][2] * inv, v[q][hh][3] * inv);
+        const f32x4 hv{bf16_lo(p0), bf16_hi(p0), bf16_lo(p1), bf16_hi(p1)};
+        *(u32x2*)(h + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane) = u32x2{p0, p1};
 #pragma unroll
         for (int k = 0; k < kNDot; ++k)
 #pragma unroll
@@ -531,6 +523,7 @@ struct EpiReluSqT {
         for (int e = 0; e < 4; ++e) v[q][e] += w.s * k * w.a[e];
       }
     }
+    u32x2 pk[R];  // the bf16 outputs, which the next linear's rank-1 dots read back
 #pragma unroll
     for (int q = 0; q < R; ++q) {
 #pragma unroll
@@ -538,16 +531,16 @@ struct EpiReluSqT {
         const float r = fmaxf(v[q][e], 0.f);
         v[q][e] = r * r;
       }
-      st_bf16x4(out + (int64_t)(row0 + q) * ldo + n0 + 4 * lane, v[q]);
+      pk[q] = u32x2{pack_bf16x2(v[q][0], v[q][1]), pack_bf16x2(v[q][2], v[q][3])};
+      *(u32x2*)(out + (int64_t)(row0 + q) * ldo + n0 + 4 * lane) = pk[q];
     }
     if (w.nr) {
       static_assert(R == 8, "warp_sum8 reduces 8 rows");
       float d[R];
 #pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const f32x4 hv = bf16_round4(v[q]);
-        d[q] = hv[0] * w.b[0] + hv[1] * w.b[1] + hv[2] * w.b[2] + hv[3] * w.b[3];
-      }
+      for (int q = 0; q < R; ++q)
+        d[q] = bf16_lo(pk[q][0]) * w.b[0] + bf16_hi(pk[q][0]) * w.b[1] + bf16_lo(pk[q][1]) * w.b[2] +
+               bf16_hi(pk[q][1]) * w.b[3];
       const float tot = warp_sum8(d, lane);
       if ((lane & 7) == 0) xb_next[(int64_t)(row0 + (lane >> 3)) * n_tiles + n_tile] = tot;
     }

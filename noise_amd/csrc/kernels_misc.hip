@@ -158,9 +158,12 @@ extern "C" int noise_credit_value(const uint16_t* q, const uint16_t* k, const fl
   a.x_sb = a.y_sb = a.v_sb = T * 64; a.x_st = a.y_st = a.v_st = 64;
   a.lse_in = lse;
   a.out = out; a.o_sb = T * 64; a.o_st = 64;
-  a.heads = 1; a.T = (int)T; a.window = window; a.hi_lo = hi_lo;
+  a.heads = 1; a.T = (int)T; a.window = window;
   NoiseTimer tm(kTimeCreditValue, (hipStream_t)stream);
-  NOISE_CHECK_HIP((launch_flash<kCredit, false, 1>(a, rows, 1, (hipStream_t)stream)));
+  if (hi_lo)
+    NOISE_CHECK_HIP((launch_flash<kCredit, true, 1>(a, rows, 1, (hipStream_t)stream)));
+  else
+    NOISE_CHECK_HIP((launch_flash<kCredit, false, 1>(a, rows, 1, (hipStream_t)stream)));
   return NOISE_OK;
 }
 

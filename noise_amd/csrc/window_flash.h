@@ -23,7 +23,7 @@
 // kCenter computes the value scores the same way as the logits, S2^T[i, o] = v_i . hub_o (v staged in LDS like y,
 // hub in registers like x), and accumulates sum_i p_i s2_i beside sum_i p_i with fp32 probabilities.
 //
-// kAttn with BOUNDED (a.bound > 0): the model normalizes q and k (RMS over 64 channels, so |q| = |k| <= 8 and
+// kAttn with OPT, bounded (a.bound > 0): the model normalizes q and k (RMS over 64 channels, so |q| = |k| <= 8 and
 // |q . k / 8| <= 8); softmax weights are then exp(s - bound) in (e^-16, ~1] with no running maximum and no rescaling.
 #pragma once
 
@@ -49,7 +49,7 @@ struct FlashArgs {
   const float* xb_vec;  // kAttn: per-batch vector base, batch b uses xb_vec + xb_row[b] * xb_stride
   const int32_t* xb_row;
   int64_t xb_stride;
-  int32_t heads, T, window, hi_lo;
+  int32_t heads, T, window;
   float bound;          // kAttn: > 0 when |x . y / 8| <= bound is guaranteed (fixed-reference softmax)
   // kAttn: the direct draws' jitter of the output (jit_sigma 0: none). Batch entry b is draw jit_draw0 + b / jit_n_seq
   // of token row jit_seq[b]; the jitter of output o, channel c of the heads * 64 comes from rng.h dust_noise_quad.
@@ -87,15 +87,16 @@ struct FlashStage<kCredit> {
 // Waves per SIMD the registers are sized for. Bounded attention (the model's forward) fits 128 VGPRs, so four
 // workgroups share a CU (4 x 32 KB of LDS); the credit value pass fits 168 (three workgroups, 3 x 48.5 KB); the other
 // modes need more registers and keep two.
-template <int MODE, bool BOUNDED>
-constexpr int kFlashOccupancy = (MODE == kAttn && BOUNDED) ? 4 : (MODE == kCredit ? 3 : 2);
+template <int MODE, bool OPT>
+constexpr int kFlashOccupancy = (MODE == kAttn && OPT) ? 4 : (MODE == kCredit && !OPT ? 3 : 2);
 
-template <int MODE, bool BOUNDED, int OG>
-__global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_flash_kernel(FlashArgs a) {
+// OPT: kAttn's bounded softmax; kCredit's value source as bf16 high and low parts (otherwise the high part only).
+template <int MODE, bool OPT, int OG>
+__global__ __launch_bounds__(256, (kFlashOccupancy<MODE, OPT>)) void window_flash_kernel(FlashArgs a) {
   constexpr int kBO = FlashTile<OG>::BO;
   __shared__ __align__(16) bf16_t ys[2][64 * 64];
   __shared__ __align__(16) bf16_t vt_hi[2][64 * 64];
-  __shared__ __align__(16) bf16_t vt_lo[MODE == kCredit ? 2 : 1][MODE == kCredit ? 64 * 64 : 4];
+  __shared__ __align__(16) bf16_t vt_lo[MODE == kCredit && OPT ? 2 : 1][MODE == kCredit && OPT ? 64 * 64 : 4];
   __shared__ float lse_s[2][64];
 
   const int T = a.T, W = a.window;
@@ -133,7 +134,8 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
 
   const bf16_t* xg = a.x + b * a.x_sb + head * 64;
   const bf16_t* yg = a.y + b * a.y_sb + head * 64;
-  constexpr bool bounded = (MODE == kAttn) && BOUNDED;
+  constexpr bool bounded = (MODE == kAttn) && OPT;
+  constexpr bool hi_lo = (MODE == kCredit) && OPT;
 
   bf16x8 xf[OG][4];
 #pragma unroll
@@ -234,13 +236,12 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const float f0 = st.v[k][2 * j], f1 = st.v[k][2 * j + 1];
-          const bf16_t h0 = f32_to_bf16(f0), h1 = f32_to_bf16(f1);
-          hi[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-          if (a.hi_lo) lo[j] = pack_bf16x2(f0 - bf16_to_f32(h0), f1 - bf16_to_f32(h1));
+          hi[j] = pack_bf16x2(f0, f1);
+          if constexpr (hi_lo) lo[j] = pack_bf16x2(f0 - bf16_lo(hi[j]), f1 - bf16_hi(hi[j]));
         }
         const int at = vt_slot(row, c4);
         *(u32x2*)(&vt_hi[s][at]) = u32x2{hi[0], hi[1]};
-        if (a.hi_lo) *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0], lo[1]};
+        if constexpr (hi_lo) *(u32x2*)(&vt_lo[s][at]) = u32x2{lo[0], lo[1]};
       }
       if (tid < 64) lse_s[s][tid] = st.lse * kLog2e;  // staged in log2 units
     } else if constexpr (MODE == kCenter || MODE == kAttn) {
@@ -416,7 +417,7 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
 #pragma unroll
               for (int og = 0; og < OG; ++og)
                 if (any[og]) o_acc[og][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[og], o_acc[og][dt], 0, 0, 0);
-              if (MODE == kCredit && a.hi_lo) {
+              if constexpr (hi_lo) {
                 const v4s ga = ds_read_tr16(&vt_lo[s][at_a]), gb = ds_read_tr16(&vt_lo[s][at_b]);
                 const bf16x8 lf = __builtin_bit_cast(bf16x8, s16x8{ga[0], ga[1], ga[2], ga[3], gb[0], gb[1], gb[2], gb[3]});
 #pragma unroll
@@ -466,13 +467,14 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
 #pragma unroll
               for (int j = 0; j < 4; ++j) jz[j] *= a.jit_sigma;
             }
-            bf16_t e[4];
+            uint32_t e[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              e[j] = f32_to_bf16(o_acc[og][dt][g * 4 + j] * inv + jz[j]);
-              if (bv) dot += bf16_to_f32(e[j]) * bv[d + j];
+            for (int j = 0; j < 2; ++j) {
+              e[j] = pack_bf16x2(o_acc[og][dt][g * 4 + 2 * j] * inv + jz[2 * j],
+                                 o_acc[og][dt][g * 4 + 2 * j + 1] * inv + jz[2 * j + 1]);
+              if (bv) dot += bf16_lo(e[j]) * bv[d + 2 * j] + bf16_hi(e[j]) * bv[d + 2 * j + 1];
             }
-            *(u32x2*)(og_ptr + d) = u32x2{(uint32_t)e[0] | ((uint32_t)e[1] << 16), (uint32_t)e[2] | ((uint32_t)e[3] << 16)};
+            *(u32x2*)(og_ptr + d) = u32x2{e[0], e[1]};
           }
         if (a.xb_out) {
           dot += lane_xor32(dot, lane);
@@ -498,10 +500,10 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, BOUNDED>)) void window_
 namespace noise {
 
 // One launch of the flash kernel over `batch` x `heads` rows of T tokens (T % 128 == 0).
-template <int MODE, bool BOUNDED, int OG>
+template <int MODE, bool OPT, int OG>
 inline hipError_t launch_flash(const FlashArgs& a, int64_t batch, int heads, hipStream_t stream) {
   constexpr int kBO = FlashTile<OG>::BO;
-  hipLaunchKernelGGL((window_flash_kernel<MODE, BOUNDED, OG>), dim3((unsigned)((a.T + kBO - 1) / kBO), (unsigned)heads,
+  hipLaunchKernelGGL((window_flash_kernel<MODE, OPT, OG>), dim3((unsigned)((a.T + kBO - 1) / kBO), (unsigned)heads,
                      (unsigned)batch), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
