@@ -54,6 +54,9 @@ __device__ __forceinline__ v4s ds_read_tr16(const bf16_t* p) {
 // soft caps whose arguments are bounded.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// 1/sqrt(x) for x >= the RMS-norm epsilon: v_rsq_f32 alone. rsqrtf adds a rescaling that changes only denormal
+// inputs, which these arguments (a mean square plus eps = 2^-23) never are.
+__device__ __forceinline__ float rsq_norm(float x) { return __builtin_amdgcn_rsqf(x); }
 
 
 // Cross-lane moves without the LDS crossbar. dpp_mov<CTRL>: a DPP row control (0xB1 quad_perm [1,0,3,2], 0x4E

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __r
 #pragma unroll
   for (int j = 0; j < 8; ++j) ss += e[j] * e[j];
   ss = warp_sum(ss);
-  const float inv = bad ? __builtin_nanf("") : rsqrtf(ss * (1.0f / kD) + kNormEps);
+  const float inv = bad ? __builtin_nanf("") : rsq_norm(ss * (1.0f / kD) + kNormEps);
   float* dst = x0 + r * kD + c0;
   *(f32x4*)dst = f32x4{e[0] * inv, e[1] * inv, e[2] * inv, e[3] * inv};
   *(f32x4*)(dst + 4) = f32x4{e[4] * inv, e[5] * inv, e[6] * inv, e[7] * inv};
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
   ss = warp_sum(ss);
-  const float inv = rsqrtf(ss * (1.0f / kD) + kNormEps);
+  const float inv = rsq_norm(ss * (1.0f / kD) + kNormEps);
   float hv[8];
   u32x4 packed;
 #pragma unroll
@@ -240,8 +240,7 @@ struct EpiQKV {
   const float* ve;    // [Vp, 512] or NULL
   int64_t off_ve;
   int Vp;
-  const float* cos_t;  // [T, 32]
-  const float* sin_t;
+  const u32x4* rope;   // [T, 16]: rope_table_kernel's per-lane rotary values
   static constexpr int kRows = kEpiRows;
   struct Wave {
     int row_base, t0, seg, c;
@@ -250,8 +249,8 @@ struct EpiQKV {
     int tok;
     f32x4 a, b_ve;
   };
-  // q / k columns: the row's cos and sin values, packed as bf16 pairs (the rotary tables hold bf16 values, so the
-  // packing is exact); v columns: the row's value-embedding values (fp32 bits) and its gate.
+  // q / k columns: the row's rotary values from the per-lane table (bf16 pairs: 4 cos, then 4 sin with the rotation's
+  // sign); v columns: the row's value-embedding values (fp32 bits) and its gate.
   struct Pre {
     u32x4 w[kEpiRows];
     float g[kEpiRows];
@@ -282,13 +281,8 @@ struct EpiQKV {
   __device__ __forceinline__ void load(int row0, int, int lane, const Wave& w, Pre& p) const {
     const int i0 = row0 - w.row_base;
     if (w.seg < 2) {
-      const int j = 4 * (lane & 7);
 #pragma unroll
-      for (int q = 0; q < kEpiRows; ++q) {
-        const f32x4 c = ld4(cos_t + (w.t0 + i0 + q) * 32 + j), sn = ld4(sin_t + (w.t0 + i0 + q) * 32 + j);
-        p.w[q] = u32x4{pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3]), pack_bf16x2(sn[0], sn[1]),
-                       pack_bf16x2(sn[2], sn[3])};
-      }
+      for (int q = 0; q < kEpiRows; ++q) p.w[q] = rope[(w.t0 + i0 + q) * 16 + (lane & 15)];
     } else if (ve) {
 #pragma unroll
       for (int q = 0; q < kEpiRows; ++q) {
@@ -310,7 +304,6 @@ struct EpiQKV {
       }
     }
     if (w.seg < 2) {
-      const bool first = (lane & 15) < 8;
 #pragma unroll
       for (int q = 0; q < R; ++q) {
         const float cs[4] = {bf16_lo(p.w[q][0]), bf16_hi(p.w[q][0]), bf16_lo(p.w[q][1]), bf16_hi(p.w[q][1])};
@@ -319,12 +312,12 @@ struct EpiQKV {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float other = dpp_mov<0x128>(v[q][e]);  // lane ^ 8: the rotary partner in the head's 16 lanes
-          v[q][e] = first ? v[q][e] * cs[e] + other * sn[e] : -other * sn[e] + v[q][e] * cs[e];
+          v[q][e] = v[q][e] * cs[e] + other * sn[e];  // sn carries the sign: - on the head's second half
           ss += v[q][e] * v[q][e];
         }
         ss = group_sum8(ss);
         ss += dpp_mov<0x140>(ss);  // the head's 16 lanes
-        const float inv = rsqrtf(ss * (1.0f / kHD) + kNormEps);
+        const float inv = rsq_norm(ss * (1.0f / kHD) + kNormEps);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[q][e] *= inv;
       }
@@ -447,7 +440,7 @@ struct EpiResidNorm {
     float dk[kNDot][R];
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      const float inv = rsqrtf(lane_val(tot, 16 * q) * (1.0f / kD) + kNormEps);
+      const float inv = rsq_norm(lane_val(tot, 16 * q) * (1.0f / kD) + kNormEps);
 #pragma unroll
       for (int k = 0; k < kNDot; ++k) dk[k][q] = 0.f;
 #pragma unroll
@@ -661,12 +654,13 @@ struct Workspace {
   float *x, *x0;
   bf16_t *h, *qkv, *y, *hid;
   float *xb, *gate, *xbp, *xb1, *psum, *tgt, *row_ce;
+  u32x4* rope;  // [T, 16] per-lane rotary values of the q|k|v epilogue
   size_t bytes;
 };
 
 static constexpr int kHeadParts = 4096 / Tile::BN;  // column tiles of the head GEMM at padded_vocab <= 4096
 
-static Workspace carve(void* base, int64_t M) {
+static Workspace carve(void* base, int64_t M, int64_t T) {
   Workspace w;
   char* p = (char*)base;
   size_t off = 0;
@@ -684,8 +678,25 @@ static Workspace carve(void* base, int64_t M) {
   w.psum = (float*)take(M * kHeadParts * 4);
   w.tgt = (float*)take(M * 4);
   w.row_ce = (float*)take(M * 4);
+  w.rope = (u32x4*)take(T * 16 * sizeof(u32x4));
   w.bytes = off;
   return w;
+}
+
+// The q|k|v epilogue's rotary values, per position t and lane l of a head's 16 (channels 4l .. 4l+3): cos of
+// frequency pair 4 (l % 8) + e as bf16 pairs, then sin with the rotation's sign, + on the first half (channels < 32)
+// and - on the second (utils/model.py:55-58). The model's tables hold bf16 values, so the packing is exact.
+__global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict__ cos_t,
+                                                         const float* __restrict__ sin_t, int64_t T,
+                                                         u32x4* __restrict__ rope) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // t * 16 + l
+  if (i >= T * 16) return;
+  const int64_t t = i >> 4;
+  const int l = (int)(i & 15), j = 4 * (l & 7);
+  const f32x4 c = *(const f32x4*)(cos_t + t * 32 + j);
+  f32x4 sn = *(const f32x4*)(sin_t + t * 32 + j);
+  if (l >= 8) sn = -sn;
+  rope[i] = u32x4{pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3]), pack_bf16x2(sn[0], sn[1]), pack_bf16x2(sn[2], sn[3])};
 }
 
 // dst[r] = src[the member's batch row, same position]: the captured block input replicated over the draws
@@ -727,7 +738,7 @@ using namespace noise;
 
 extern "C" size_t noise_population_forward_workspace(int64_t members, int64_t T) {
   if (members <= 0 || T <= 0) return 0;
-  return carve(nullptr, members * T).bytes;
+  return carve(nullptr, members * T, T).bytes;
 }
 
 // The direct draws' part of a forward (train/val/dust.py:195-233): a clean pass that captures every block's input
@@ -773,7 +784,7 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
                     model->x0_lambdas, "model weight pointer is NULL");
   const int64_t M = members * T;
   NOISE_REQUIRE(M <= (int64_t)INT32_MAX / 4, "members * T = %lld too large", (long long)M);
-  Workspace ws = carve(workspace, M);
+  Workspace ws = carve(workspace, M, T);
   NOISE_REQUIRE(workspace && workspace_bytes >= ws.bytes, "workspace %zu bytes < %zu", workspace_bytes, ws.bytes);
   int rc = prepare_all();
   if (rc) return rc;
@@ -789,6 +800,9 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
   const bool from_block = dr->entry >= 0;  // rerun from a captured block input
   const int first_layer = from_block ? dr->entry : 0;
 
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((T * 16 + 255) / 256)), dim3(256), 0, stream, model->rope_cos,
+                     model->rope_sin, T, ws.rope);
+  NOISE_LAUNCH_CHECK();
   if (from_block) {
     hipLaunchKernelGGL(replicate_rows_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, dr->x_in, ws.x, M);
     NOISE_LAUNCH_CHECK();
@@ -834,7 +848,7 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
                                      hipMemcpyDeviceToDevice, stream));
 
     EpiQKV eq{mb, ws.qkv, {pert->c_q[i], pert->c_k[i], pert->c_v[i]}, ws.xb, L.w_gate ? ws.gate : nullptr, L.ve,
-              pert->ve[i], Vp, model->rope_cos, model->rope_sin};
+              pert->ve[i], Vp, ws.rope};
     {
       NoiseTimer tm(kTimeQKV, stream);
       NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_qkv, kD, (int)M, kQKV, kD, eq, stream)));
@@ -964,7 +978,7 @@ extern "C" int noise_population_forward(const noise_gpt* model, const noise_pert
 extern "C" size_t noise_dust_workspace(int64_t n_draws, int64_t n_seq, int64_t T) {
   if (n_draws <= 0 || n_seq <= 0 || T <= 0) return 0;
   const int64_t members = n_draws * n_seq;
-  return align256((size_t)members * 4) + carve(nullptr, members * T).bytes;
+  return align256((size_t)members * 4) + carve(nullptr, members * T, T).bytes;
 }
 
 // members = n_draws * n_seq (draw-major, member m on batch row m % n_seq), clean weights; per-token CE out
