@@ -262,13 +262,7 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   auto frag = [&](int off) { return *(const bf16x8*)(smem_raw + off); };
   constexpr int kTileStride = 32 * S::BK * 2;  // bytes between the 32-row MFMA tiles of a stage
 
-  f32x16 acc[S::TM][S::TN];
-#pragma unroll
-  for (int i = 0; i < S::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < S::TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  f32x16 acc[S::TM][S::TN];  // first written by step 0's first MFMAs, which take a zero accumulator
 
   // Prologue: steps 0 .. NS - 1 in flight; stage 0 visible; its first k-substep's fragments read.
 #pragma unroll
@@ -286,7 +280,9 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   // kt % NS with step kt + NS; read the next step's k-substep 0 and multiply k-substep 1.
   // The reads and loads of each half are spread between its MFMAs (one per MFMA), so that neither the LDS nor the
   // texture-address queue sees a burst.
-  for (int kt = 0; kt < nk; ++kt) {
+  // Step 0 is peeled: its first MFMAs take the inline constant 0 as the accumulator, so the accumulators need no
+  // zeroing moves.
+  auto step = [&](int kt, auto first) {
     const int pb = (kt % NS) * kStage;
 #pragma unroll
     for (int i = 0; i < S::TM; ++i) f1a[i] = frag(fa_off[1] + pb + i * kTileStride);
@@ -296,7 +292,8 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
     for (int i = 0; i < S::TM; ++i)
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0a[i], f0b[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0a[i], f0b[j], decltype(first)::value ? f32x16{} : acc[i][j],
+                                                            0, 0, 0);
     first_half_schedule<S>();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -316,7 +313,9 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1a[i], f1b[j], acc[i][j], 0, 0, 0);
     second_half_schedule<S>();
     __builtin_amdgcn_sched_barrier(0);
-  }
+  };
+  step(0, std::true_type{});
+  for (int kt = 1; kt < nk; ++kt) step(kt, std::false_type{});
   wait_vmcnt_imm<0>();  // the loads issued past the last step have landed
   __syncthreads();      // every wave is done with the stages before the epilogue reuses the LDS
 
