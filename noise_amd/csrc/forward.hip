@@ -52,41 +52,65 @@ struct Jitter {
 };
 
 // ---------------------------------------------------------------------------------------------------------------
-// x0 = norm(wte[tok] + sign a[tok] b [+ the direct draws' jitter])  (eggroll.py:61-63, 74; dust.py:218-220); one wave
-// per row, 8 channels per lane.
+// x0 = norm(wte[tok] + sign a[tok] b [+ the direct draws' jitter])  (eggroll.py:61-63, 74; dust.py:218-220); 8 rows
+// per wave, 8 channels per lane.
 __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __restrict__ wte, int Vp, int64_t off_wte,
                                                     Jitter jit, float* __restrict__ x0, int64_t M) {
-  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= M) return;
+  // 8 consecutive rows per wave (M and the member length are multiples of 8, so they belong to one member): lanes
+  // 0..7 fetch the rows' tokens and noise scalars together, the member's b vector is read once, and the 8 embedding
+  // rows are loaded before any is reduced, so the dependent loads (member table, token, embedding row) overlap.
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8;
+  if (r0 >= M) return;
   const int lane = threadIdx.x & 63, c0 = lane * 8;
-  const int m = mb.member(r);
-  int64_t tok = mb.token(r);
-  const bool bad = tok < 0 || tok >= Vp;
-  if (bad) tok = 0;
+  const int m = mb.member(r0);
   const float* nr = mb.nrow(m);
   const float s = mb.sgn(m);
-  const float at = nr ? s * nr[off_wte + tok] : 0.f;
-  float e[8], ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    e[j] = wte[tok * kD + c0 + j];
-    if (nr) e[j] += at * nr[off_wte + Vp + c0 + j];
+  int tk = 0, bad = 0;
+  float at = 0.f;
+  if (lane < 8) {
+    const int64_t t = mb.token(r0 + lane);
+    bad = t < 0 || t >= Vp;
+    tk = bad ? 0 : (int)t;
+    if (nr) at = s * nr[off_wte + tk];
   }
-  if (jit.on()) {
+  float b[8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f32x4 z = jit.quad(mb, r, kD, c0 + 4 * h);
+  for (int j = 0; j < 8; ++j) b[j] = nr ? nr[off_wte + Vp + c0 + j] : 0.f;
+  float e[8][8], ss[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) e[4 * h + j] += z[j];
+  for (int q = 0; q < 8; ++q) {
+    const int tq = lane_val(tk, q);
+    const f32x4 w0 = *(const f32x4*)(wte + (int64_t)tq * kD + c0), w1 = *(const f32x4*)(wte + (int64_t)tq * kD + c0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { e[q][j] = w0[j]; e[q][4 + j] = w1[j]; }
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float aq = lane_val(at, q);
+    if (nr) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[q][j] += aq * b[j];
     }
-  }
+    if (jit.on()) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ss += e[j] * e[j];
-  ss = warp_sum(ss);
-  const float inv = bad ? __builtin_nanf("") : rsq_norm(ss * (1.0f / kD) + kNormEps);
-  float* dst = x0 + r * kD + c0;
-  *(f32x4*)dst = f32x4{e[0] * inv, e[1] * inv, e[2] * inv, e[3] * inv};
-  *(f32x4*)(dst + 4) = f32x4{e[4] * inv, e[5] * inv, e[6] * inv, e[7] * inv};
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 z = jit.quad(mb, r0 + q, kD, c0 + 4 * h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[q][4 * h + j] += z[j];
+      }
+    }
+    ss[q] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss[q] += e[q][j] * e[q][j];
+  }
+  const float tot = warp_sum8(ss, lane);  // lane l: row (l >> 3) & 7
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float inv = lane_val(bad, q) ? __builtin_nanf("") : rsq_norm(lane_val(tot, 8 * q) * (1.0f / kD) + kNormEps);
+    float* dst = x0 + (r0 + q) * kD + c0;
+    *(f32x4*)dst = f32x4{e[q][0] * inv, e[q][1] * inv, e[q][2] * inv, e[q][3] * inv};
+    *(f32x4*)(dst + 4) = f32x4{e[q][4] * inv, e[q][5] * inv, e[q][6] * inv, e[q][7] * inv};
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -810,7 +834,7 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
     NOISE_LAUNCH_CHECK();
   } else {
     NoiseTimer tm(kTimeEmbed, stream);
-    hipLaunchKernelGGL(embed_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte,
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte,
                        dr->jit(-1, 0), ws.x0, M);
     NOISE_LAUNCH_CHECK();
   }
