@@ -55,7 +55,8 @@ struct Jitter {
 // x0 = norm(wte[tok] + sign a[tok] b [+ the direct draws' jitter])  (eggroll.py:61-63, 74; dust.py:218-220); 8 rows
 // per wave, 8 channels per lane.
 __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __restrict__ wte, int Vp, int64_t off_wte,
-                                                    Jitter jit, float* __restrict__ x0, int64_t M) {
+                                                    Jitter jit, float* __restrict__ x0, float* __restrict__ x0_inv,
+                                                    int64_t M) {
   // 8 consecutive rows per wave (M and the member length are multiples of 8, so they belong to one member): lanes
   // 0..7 fetch the rows' tokens and noise scalars together, the member's b vector is read once, and the 8 embedding
   // rows are loaded before any is reduced, so the dependent loads (member table, token, embedding row) overlap.
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __r
     const float aq = lane_val(at, q);
     if (nr) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) e[q][j] += aq * b[j];
+      for (int j = 0; j < 8; ++j) e[q][j] = fmaf(aq, b[j], e[q][j]);  // the mlp_proj epilogue's x0 recompute repeats this
     }
     if (jit.on()) {
 #pragma unroll
@@ -107,6 +108,7 @@ __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __r
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const float inv = lane_val(bad, q) ? __builtin_nanf("") : rsq_norm(lane_val(tot, 8 * q) * (1.0f / kD) + kNormEps);
+    if (lane == q) x0_inv[r0 + q] = inv;
     float* dst = x0 + (r0 + q) * kD + c0;
     *(f32x4*)dst = f32x4{e[q][0] * inv, e[q][1] * inv, e[q][2] * inv, e[q][3] * inv};
     *(f32x4*)(dst + 4) = f32x4{e[q][4] * inv, e[q][5] * inv, e[q][6] * inv, e[q][7] * inv};
@@ -365,7 +367,7 @@ struct EpiQKV {
 // holds whole 512-wide rows (512-column tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3. Groups of
 // 4 rows keep the x and x0 prefetch small. The rank-1 term is added unconditionally: its a and dot are zero for rows
 // without noise.
-template <bool kMix, int kNDot, bool kJit = false>
+template <bool kMix, int kNDot, bool kJit = false, bool kX0 = false>
 struct EpiResidNorm {
   static constexpr int kRows = 4;
   Members mb;
@@ -373,7 +375,13 @@ struct EpiResidNorm {
   const float* xbp;     // [M, nxb] partial dots of this linear's input with its b
   int nxb;
   int64_t off;          // noise offset of this linear's a
-  const float* x0;      // [M, 512] (mix only)
+  const float* x0;      // [M, 512] (mix only; kX0: recomputed instead)
+  // kX0: the mix's x0 recomputed as (wte[tok] + sign a[tok] b) * x0_inv, exactly as embed_kernel forms it, from the
+  // embedding row (cache-resident table) instead of a 2 KB HBM read per row
+  const float* wte;
+  const float* x0_inv;  // [M] embed_kernel's per-row norm scale
+  int Vp;
+  int64_t off_wte;
   const float* resid_lambdas;
   const float* x0_lambdas;
   int layer;            // the block whose lambdas mix
@@ -387,6 +395,9 @@ struct EpiResidNorm {
     const float* nr;
     float s, d, lr, l0;
     f32x4 a[2], b[kNDot][2];
+    int tok;         // kX0, by lane: the row's token, its noise scalar sign a[tok] and norm scale
+    float at, inv;
+    f32x4 bw[2];     // kX0: the embedding's b vector at this lane's columns
   };
   struct Pre {
     f32x4 xv[kRows][2], x0v[kRows][2];
@@ -413,6 +424,20 @@ struct EpiResidNorm {
         for (int k = 0; k < kNDot; ++k) w.b[k][hh] = ld4(w.nr + off_b[k] + hh * 256 + 4 * lane);
       }
     }
+    if constexpr (kX0) {
+      w.tok = 0; w.at = 0.f; w.inv = 0.f;
+      w.bw[0] = w.bw[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (lane < nrows) {
+        const int64_t t = mb.token(row_base + lane);
+        w.tok = (t < 0 || t >= Vp) ? 0 : (int)t;
+        w.inv = x0_inv[row_base + lane];
+        if (w.nr) w.at = w.s * w.nr[off_wte + w.tok];
+      }
+      if (w.nr) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) w.bw[hh] = ld4(w.nr + off_wte + Vp + hh * 256 + 4 * lane);
+      }
+    }
     w.lr = 1.f; w.l0 = 0.f;
     if (kMix) {
       w.lr = resid_lambdas[layer];
@@ -420,14 +445,17 @@ struct EpiResidNorm {
       if (w.nr) { w.lr += w.s * w.nr[off_resid + layer]; w.l0 += w.s * w.nr[off_x0 + layer]; }
     }
   }
-  __device__ __forceinline__ void load(int row0, int, int lane, const Wave&, Pre& p) const {
+  __device__ __forceinline__ void load(int row0, int, int lane, const Wave& w, Pre& p) const {
 #pragma unroll
-    for (int q = 0; q < kRows; ++q)
+    for (int q = 0; q < kRows; ++q) {
+      const int tq = kX0 ? lane_val(w.tok, row0 - w.row_base + q) : 0;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         p.xv[q][hh] = ld4(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
-        if (kMix) p.x0v[q][hh] = ld4(x0 + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
+        if (kX0) p.x0v[q][hh] = ld4(wte + (int64_t)tq * kD + hh * 256 + 4 * lane);  // the embedding row
+        else if (kMix) p.x0v[q][hh] = ld4(x0 + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
       }
+    }
   }
   template <int R>
   __device__ __forceinline__ void rows(int row0, int, int, int lane, const Wave& w, const Pre& p,
@@ -444,6 +472,7 @@ struct EpiResidNorm {
 #pragma unroll
     for (int q = 0; q < R; ++q) {
       const float d = lane_val(w.d, i0 + q);
+      const float at = kX0 ? lane_val(w.at, i0 + q) : 0.f, inv = kX0 ? lane_val(w.inv, i0 + q) : 0.f;
       ss[q] = 0.f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -453,7 +482,8 @@ struct EpiResidNorm {
           float val = v[q][hh][e];
           val += w.s * d * w.a[hh][e];
           xn[e] += val;
-          if (kMix) xn[e] = w.lr * xn[e] + w.l0 * p.x0v[q][hh][e];
+          const float x0e = kX0 ? fmaf(at, w.bw[hh][e], p.x0v[q][hh][e]) * inv : p.x0v[q][hh][e];
+          if (kMix) xn[e] = w.lr * xn[e] + w.l0 * x0e;
           ss[q] += xn[e] * xn[e];
         }
         v[q][hh] = xn;
@@ -679,6 +709,7 @@ struct Workspace {
   bf16_t *h, *qkv, *y, *hid;
   float *xb, *gate, *xbp, *xb1, *psum, *tgt, *row_ce;
   u32x4* rope;  // [T, 16] per-lane rotary values of the q|k|v epilogue
+  float* x0_inv;  // [M] embed_kernel's per-row norm scale (the mlp_proj epilogue recomputes x0 from it)
   size_t bytes;
 };
 
@@ -702,6 +733,7 @@ static Workspace carve(void* base, int64_t M, int64_t T) {
   w.psum = (float*)take(M * kHeadParts * 4);
   w.tgt = (float*)take(M * 4);
   w.row_ce = (float*)take(M * 4);
+  w.x0_inv = (float*)take(M * 4);
   w.rope = (u32x4*)take(T * 16 * sizeof(u32x4));
   w.bytes = off;
   return w;
@@ -751,6 +783,7 @@ static int prepare_all() {
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiReluSqT<true>>()));
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<false, 1, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3, true>>()));
+  NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3, false, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiHeadCE>()));
   g_prepared = true;
   return NOISE_OK;
@@ -823,6 +856,8 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
   if (!dr) dr = &none;
   const bool from_block = dr->entry >= 0;  // rerun from a captured block input
   const int first_layer = from_block ? dr->entry : 0;
+  // the λ mix recomputes x0 from the embedding table when this call's embed_kernel formed it without jitter
+  const bool x0_recompute = !from_block && !dr->jit(-1, 0).on();
 
   hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((T * 16 + 255) / 256)), dim3(256), 0, stream, model->rope_cos,
                      model->rope_sin, T, ws.rope);
@@ -835,7 +870,7 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
   } else {
     NoiseTimer tm(kTimeEmbed, stream);
     hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte,
-                       dr->jit(-1, 0), ws.x0, M);
+                       dr->jit(-1, 0), ws.x0, ws.x0_inv, M);
     NOISE_LAUNCH_CHECK();
   }
   if (dr->capture)
@@ -962,6 +997,11 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
         memcpy((void*)&ej, (const void*)&em, sizeof(em));
         ej.jit = jm;
         NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, ej, stream)));
+      } else if (x0_recompute) {
+        EpiResidNorm<true, 3, false, true> ex;
+        memcpy((void*)&ex, (const void*)&em, sizeof(em));
+        ex.wte = model->wte; ex.x0_inv = ws.x0_inv; ex.Vp = Vp; ex.off_wte = pert->wte;
+        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, ex, stream)));
       } else {
         NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.hid, kF, L.w_mlp_proj, kF, (int)M, kD, kF, em, stream)));
       }

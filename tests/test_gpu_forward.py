@@ -96,6 +96,33 @@ def test_population_loss_matches_oracle(dev):
     assert np.corrcoef(d_ref, d_got)[0, 1] > 0.9, (d_ref, d_got)
 
 
+def test_population_embedding_noise_reaches_every_mix(dev):
+    """Only the embedding perturbed (sigma 2), and every block's lambda mix weighting x0 by 1: the antithetic loss
+    differences then carry x0's perturbation through every mix, which the kernels recompute from the embedding table
+    in the MLP projection's epilogue. A recompute without the member's noise term (planted in the oracle: the mixes
+    of blocks 1..7 with the unperturbed x0) moves these differences by up to 0.08; the bound is 0.01."""
+    from noise_amd.population import population_loss
+    print('population loss, embedding noise only, m=8 T=256', flush=True)
+    ocfg, gcfg = _cfgs()
+    w = dict(_weights(ocfg))
+    w['x0_lambdas'] = torch.ones_like(w['x0_lambdas'])
+    model = _model(dev, w, gcfg)
+    members, sigma = 8, 2.0
+    noise = recipe.population_noise(ocfg, members, seed=78, step=1)
+    wte = 'transformer.wte.weight'
+    noise = {k: v if k == wte else (tuple(torch.zeros_like(t) for t in v) if isinstance(v, tuple) else torch.zeros_like(v))
+             for k, v in noise.items()}
+    sign = torch.tensor([sigma, -sigma] * (members // 2))
+    idx, tg = recipe.tokens(ocfg, batch=1, seed=32)
+    ref = om.population_loss(w, ocfg, noise, sign, idx[0], tg[0]) / SEQ
+    dnoise = {k: tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for k, v in noise.items()}
+    got = population_loss(model, None, dnoise, sign.to(dev), idx[0].to(dev), tg[0].to(dev)).cpu()
+    assert ((got - ref).abs() / ref.abs()).max().item() < 1e-2, (got, ref)
+    d_ref, d_got = ref[0::2] - ref[1::2], got[0::2] - got[1::2]
+    print('antithetic differences', d_ref.tolist(), d_got.tolist(), flush=True)
+    assert (d_got - d_ref).abs().max().item() < 0.01, (d_got, d_ref)
+
+
 def test_lowrank_matches_bruteforce(dev):
     """x (W + s a b^T)^T with the perturbed weight materialized, on the CPU."""
     from noise_amd.population import lowrank
