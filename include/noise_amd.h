@@ -137,6 +137,14 @@ int noise_fitness(const float* losses, int64_t members, int64_t pairs, float* fi
 int noise_outer_grad(const float* rows, int64_t stride, int64_t a_off, int64_t b_off, const float* weight,
                      int64_t pairs, int64_t out, int64_t in, float scale, float* grad, void* stream);
 
+/* noise_outer_grad for n matrices in one launch (fp32 MFMA, 128 x 128 output tiles; each matrix j as noise_outer_grad
+ * with a_off[j], b_off[j] >= 0, out[j], in[j] and grads[j], a host array of device pointers). The per-parameter loop
+ * of the update becomes one grid that fills the GPU even where single matrices are small (512 x 512).
+ * Replaces: archive/10M/train/val/eggroll.py:155-163 (the loop over parameters and chunks of directions). */
+int noise_outer_grad_batch(const float* rows, int64_t stride, const float* weight, int64_t pairs, int32_t n,
+                           const int64_t* a_off, const int64_t* b_off, const int64_t* out, const int64_t* in,
+                           float* const* grads, float scale, void* stream);
+
 /* One AdamW step on n fp32 elements in place (torch.optim.AdamW arithmetic): p *= 1 - lr wd; m = lerp(m, g, 1-b1);
  * v = b2 v + (1 - b2) g^2; p -= lr / (1 - b1^step) * m / (sqrt(v) / sqrt(1 - b2^step) + eps).
  * shadow (optional): bf16 copy of the updated p. Replaces: archive/10M/train/val/eggroll.py:205, 167 and

@@ -56,6 +56,7 @@ _SIGNATURES = {
                                   c_p, c_p, c_p, i64, c_p, c_p, c_p, c_p, szt, c_p], ctypes.c_int),
     'noise_fitness': ([c_p, i64, i64, c_p, c_p, c_p], ctypes.c_int),
     'noise_outer_grad': ([c_p, i64, i64, i64, c_p, i64, i64, i64, f32, c_p, c_p], ctypes.c_int),
+    'noise_outer_grad_batch': ([c_p, i64, c_p, i64, ctypes.c_int32, c_p, c_p, c_p, c_p, c_p, f32, c_p], ctypes.c_int),
     'noise_adamw': ([c_p, c_p, c_p, c_p, i64, f32, f32, f32, f32, f32, i64, c_p, c_p], ctypes.c_int),
     'noise_credit_lse': ([c_p, c_p, i64, i64, i32, c_p, c_p], ctypes.c_int),
     'noise_credit_value': ([c_p, c_p, c_p, c_p, i64, i64, i32, i32, c_p, c_p], ctypes.c_int),

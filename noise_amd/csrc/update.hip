@@ -1,6 +1,7 @@
 // Fitness, gradient assembly and the AdamW step of the EGGROLL update
 // (archive/10M/train/val/eggroll.py:151-167; optimizer semantics of torch.optim.AdamW as built at :205).
 #include <math.h>
+#include <string.h>
 
 #include "common.h"
 
@@ -49,59 +50,135 @@ __global__ __launch_bounds__(1024) void fitness_kernel(const float* __restrict__
   }
 }
 
-// grad[o, i] = scale sum_j w_j a_j[o] b_j[i]: fp32 tiles of 64 x 64 outputs, 4 x 4 per thread, 16 directions per step.
-__global__ __launch_bounds__(256) void outer_grad_kernel(const float* __restrict__ rows, int64_t stride, int64_t a_off,
-                                                         int64_t b_off, const float* __restrict__ weight, int64_t pairs,
-                                                         int64_t out, int64_t in, float scale, float* __restrict__ grad) {
-  __shared__ float as[16][64];
-  __shared__ float bs[16][64];
-  const int o0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
-  const int tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
-  float acc[4][4] = {};
-  for (int64_t j0 = 0; j0 < pairs; j0 += 16) {
-    for (int e = tid; e < 16 * 64; e += 256) {
-      const int jj = e / 64, c = e % 64;
-      const int64_t j = j0 + jj;
-      float av = 0.f, bv = 0.f;
-      if (j < pairs) {
-        const float* row = rows + j * stride;
-        av = (o0 + c < out) ? row[a_off + o0 + c] : 0.f;
-        bv = (i0 + c < in) ? weight[j] * row[b_off + i0 + c] : 0.f;
+// grad[o, i] = scale sum_j w_j a_j[o] b_j[i] (eggroll.py:159-161: (w a)^T b over the pairs), on fp32 MFMA
+// (v_mfma_f32_32x32x2_f32, full fp32 products and sums). A workgroup owns a 128 x 128 output tile, each of its 4 waves
+// 64 x 64 (2 x 2 MFMA tiles); the pairs stream through two LDS stages of 16: a_j[o0 .. o0+127] and w_j b_j[i0 ..]
+// as rows [pair][128] padded to 160 floats, so the two pair rows of one operand read (lanes 0..31 and 32..63) fall
+// in opposite halves of the 64 banks. Every load is a 256-byte row segment (thread: one column, 8 of the 16 rows);
+// columns past out / in and pairs past the last read as zeros, so offsets and sizes need no alignment.
+// One launch covers a list of matrices (jobs, by value in the kernel arguments): workgroup b takes tile b - tile0 of
+// the job whose tile range holds b, tiles in row-major order over ceil(out / 128) x ceil(in / 128).
+constexpr int kOgTile = 128, kOgK = 16, kOgPitch = 160, kOgMaxJobs = 64;
+
+struct OgJob {
+  int64_t a_off, b_off;  // slice offsets of a (out values) and b (in values) in a noise row
+  int32_t out, in;
+  int32_t tile0, n_in_tiles;
+  float* grad;           // [out, in]
+};
+struct OgJobs {
+  int32_t n;
+  OgJob job[kOgMaxJobs];
+};
+
+__global__ __launch_bounds__(256) void outer_grad_kernel(const float* __restrict__ rows, int64_t stride,
+                                                         const float* __restrict__ weight, int64_t pairs, float scale,
+                                                         OgJobs jobs) {
+  __shared__ float as[2][kOgK][kOgPitch];
+  __shared__ float bs[2][kOgK][kOgPitch];
+  int jb = 0;
+  while (jb + 1 < jobs.n && (int)blockIdx.x >= jobs.job[jb + 1].tile0) ++jb;
+  const OgJob& job = jobs.job[jb];
+  const int64_t a_off = job.a_off, b_off = job.b_off, out = job.out, in = job.in;
+  float* __restrict__ grad = job.grad;
+  const int tile = (int)blockIdx.x - job.tile0;
+  const int64_t o0 = (int64_t)(tile / job.n_in_tiles) * kOgTile, i0 = (int64_t)(tile % job.n_in_tiles) * kOgTile;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wo = (wave >> 1) * 64, wi = (wave & 1) * 64;
+  const int col = tid & 127, row0 = tid >> 7;  // loader: column col of rows row0, row0 + 2, ..., row0 + 14
+  const bool a_in = o0 + col < out, b_in = i0 + col < in;
+
+  float ra[8], rb[8];
+  auto load = [&](int64_t j0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t j = j0 + row0 + 2 * q;
+      const bool live = j < pairs;
+      const float* row = rows + (live ? j : 0) * stride;
+      ra[q] = (live && a_in) ? row[a_off + o0 + col] : 0.f;
+      rb[q] = (live && b_in) ? weight[j] * row[b_off + i0 + col] : 0.f;
+    }
+  };
+  auto store = [&](int st) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      as[st][row0 + 2 * q][col] = ra[q];
+      bs[st][row0 + 2 * q][col] = rb[q];
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[u][v][r] = 0.f;
+
+  load(0);
+  store(0);
+  __syncthreads();
+  const int64_t n_steps = (pairs + kOgK - 1) / kOgK;
+  const int kr = lane >> 5, lc = lane & 31;  // operand lane: pair row kr of the k pair, column lc of the 32
+  for (int64_t t = 0; t < n_steps; ++t) {
+    const int st = (int)(t & 1);
+    const bool more = t + 1 < n_steps;
+    if (more) load((t + 1) * kOgK);
+#pragma unroll
+    for (int s = 0; s < kOgK / 2; ++s) {
+      float fa[2], fb[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        fa[u] = as[st][2 * s + kr][wo + 32 * u + lc];
+        fb[u] = bs[st][2 * s + kr][wi + 32 * u + lc];
       }
-      as[jj][c] = av;
-      bs[jj][c] = bv;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) acc[u][v] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[u], fb[v], acc[u][v], 0, 0, 0);
     }
-    __syncthreads();
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      float a4[4], b4[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) { a4[u] = as[jj][ty * 4 + u]; b4[u] = bs[jj][tx * 4 + u]; }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[u][v] += a4[u] * b4[v];
-    }
+    if (more) store(st ^ 1);
     __syncthreads();
   }
+
+  // accumulator register r of tile (u, v): row 8 (r / 4) + 4 (lane / 32) + r % 4, column lane % 32
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t o = o0 + ty * 4 + u, i = i0 + tx * 4 + v;
-      if (o < out && i < in) grad[o * in + i] = scale * acc[u][v];
-    }
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t o = o0 + wo + 32 * u + 8 * (r >> 2) + 4 * kr + (r & 3), i = i0 + wi + 32 * v + lc;
+        if (o < out && i < in) grad[o * in + i] = scale * acc[u][v][r];
+      }
 }
 
-// grad[i] = scale sum_j w_j eps_j[i] (1-D parameters: eggroll.py:163)
-__global__ void vector_grad_kernel(const float* __restrict__ rows, int64_t stride, int64_t a_off,
-                                   const float* __restrict__ weight, int64_t pairs, int64_t n, float scale,
-                                   float* __restrict__ grad) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float s = 0.f;
-  for (int64_t j = 0; j < pairs; ++j) s += weight[j] * rows[j * stride + a_off + i];
-  grad[i] = scale * s;
+// grad[i] = scale sum_j w_j eps_j[i] (1-D parameters: eggroll.py:163). A block owns 8 consecutive elements; its 256
+// threads take the pairs j = t, t + 256, ... and a fixed-order tree in LDS adds their partial sums (deterministic).
+__global__ __launch_bounds__(256) void vector_grad_kernel(const float* __restrict__ rows, int64_t stride, int64_t a_off,
+                                                          const float* __restrict__ weight, int64_t pairs, int64_t n,
+                                                          float scale, float* __restrict__ grad) {
+  __shared__ float red[256][9];
+  const int tid = threadIdx.x;
+  const int64_t i0 = (int64_t)blockIdx.x * 8;
+  float acc[8] = {};
+  for (int64_t j = tid; j < pairs; j += 256) {
+    const float wj = weight[j];
+    const float* row = rows + j * stride + a_off + i0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e < n) acc[e] += wj * row[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[tid][e] = acc[e];
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if (tid < w)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[tid][e] += red[tid + w][e];
+    __syncthreads();
+  }
+  if (tid < 8 && i0 + tid < n) grad[i0 + tid] = scale * red[0][tid];
 }
 
 struct AdamScalars {
@@ -153,18 +230,47 @@ extern "C" int noise_outer_grad(const float* rows, int64_t stride, int64_t a_off
                                 int64_t pairs, int64_t out, int64_t in, float scale, float* grad, void* stream) {
   NOISE_REQUIRE(rows && weight && grad, "NULL pointer argument");
   NOISE_REQUIRE(pairs > 0 && in > 0 && a_off >= 0 && stride > 0, "bad sizes");
+  if (b_off >= 0)  // a matrix: a one-job launch of the grouped kernel
+    return noise_outer_grad_batch(rows, stride, weight, pairs, 1, &a_off, &b_off, &out, &in, &grad, scale, stream);
+  NOISE_REQUIRE(a_off + in <= stride, "slice beyond the noise row");
   NoiseTimer tm(kTimeUpdate, (hipStream_t)stream);
-  if (b_off < 0) {
-    NOISE_REQUIRE(a_off + in <= stride, "slice beyond the noise row");
-    hipLaunchKernelGGL(vector_grad_kernel, dim3((unsigned)((in + 255) / 256)), dim3(256), 0, (hipStream_t)stream, rows,
-                       stride, a_off, weight, pairs, in, scale, grad);
-  } else {
-    NOISE_REQUIRE(out > 0 && a_off + out <= stride && b_off + in <= stride, "slice beyond the noise row");
-    dim3 grid((unsigned)((in + 63) / 64), (unsigned)((out + 63) / 64));
-    hipLaunchKernelGGL(outer_grad_kernel, grid, dim3(256), 0, (hipStream_t)stream, rows, stride, a_off, b_off, weight,
-                       pairs, out, in, scale, grad);
-  }
+  hipLaunchKernelGGL(vector_grad_kernel, dim3((unsigned)((in + 7) / 8)), dim3(256), 0, (hipStream_t)stream, rows,
+                     stride, a_off, weight, pairs, in, scale, grad);
   NOISE_LAUNCH_CHECK();
+  return NOISE_OK;
+}
+
+extern "C" int noise_outer_grad_batch(const float* rows, int64_t stride, const float* weight, int64_t pairs,
+                                      int32_t n, const int64_t* a_off, const int64_t* b_off, const int64_t* out,
+                                      const int64_t* in, float* const* grads, float scale, void* stream) {
+  NOISE_REQUIRE(rows && weight && a_off && b_off && out && in && grads, "NULL pointer argument");
+  NOISE_REQUIRE(pairs > 0 && stride > 0 && n >= 0, "bad sizes");
+  for (int32_t j = 0; j < n; ++j) {  // every matrix is checked before anything is launched
+    NOISE_REQUIRE(grads[j], "NULL gradient pointer (matrix %d)", j);
+    NOISE_REQUIRE(out[j] > 0 && in[j] > 0 && out[j] <= INT32_MAX && in[j] <= INT32_MAX, "matrix %d: bad shape", j);
+    NOISE_REQUIRE(a_off[j] >= 0 && b_off[j] >= 0 && a_off[j] + out[j] <= stride && b_off[j] + in[j] <= stride,
+                  "matrix %d: slice beyond the noise row", j);
+  }
+  NoiseTimer tm(kTimeUpdate, (hipStream_t)stream);
+  for (int32_t j0 = 0; j0 < n; j0 += kOgMaxJobs) {
+    OgJobs jobs;
+    memset(&jobs, 0, sizeof(jobs));
+    jobs.n = n - j0 < kOgMaxJobs ? n - j0 : kOgMaxJobs;
+    int64_t tiles = 0;
+    for (int k = 0; k < jobs.n; ++k) {
+      const int32_t j = j0 + k;
+      OgJob& g = jobs.job[k];
+      g.a_off = a_off[j]; g.b_off = b_off[j]; g.out = (int32_t)out[j]; g.in = (int32_t)in[j]; g.grad = grads[j];
+      g.n_in_tiles = (int32_t)((in[j] + kOgTile - 1) / kOgTile);
+      g.tile0 = (int32_t)tiles;
+      tiles += (int64_t)g.n_in_tiles * ((out[j] + kOgTile - 1) / kOgTile);
+      NOISE_REQUIRE(tiles <= INT32_MAX, "too many tiles");
+    }
+    if (tiles == 0) continue;
+    hipLaunchKernelGGL(outer_grad_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, rows, stride,
+                       weight, pairs, scale, jobs);
+    NOISE_LAUNCH_CHECK();
+  }
   return NOISE_OK;
 }
 

@@ -247,16 +247,22 @@ class Eggroll:
         _lib.call('noise_fitness', _lib.ptr(losses), losses.numel(), self.pairs, _lib.ptr(fitness), _lib.ptr(weight),
                   _lib.stream(self.device))
         optimizer.zero_grad(set_to_none=True)
+        grads, mats = {}, []
         for name, shape, c0 in zip(self.layout.names, self.layout.shapes, self.layout.col0):
-            p = self.params[name]
-            grad = torch.empty(shape, dtype=torch.float32, device=self.device)
+            grads[name] = grad = torch.empty(shape, dtype=torch.float32, device=self.device)
             if len(shape) == 2:
-                _lib.call('noise_outer_grad', _lib.ptr(rows), self.layout.stride, c0, c0 + shape[0], _lib.ptr(weight),
-                          self.pairs, shape[0], shape[1], -1.0 / n_fit, _lib.ptr(grad), _lib.stream(self.device))
+                mats.append((c0, c0 + shape[0], shape[0], shape[1], grad))
             else:
                 _lib.call('noise_outer_grad', _lib.ptr(rows), self.layout.stride, c0, -1, _lib.ptr(weight),
                           self.pairs, 1, shape[0], -1.0 / n_fit, _lib.ptr(grad), _lib.stream(self.device))
-            p.grad = grad.to(p.dtype)
+        # every matrix's outer-product sum in one grouped launch (eggroll.py:155-163)
+        arr = lambda vals, t: (t * len(vals))(*vals)
+        _lib.call('noise_outer_grad_batch', _lib.ptr(rows), self.layout.stride, _lib.ptr(weight), self.pairs, len(mats),
+                  arr([m[0] for m in mats], ctypes.c_int64), arr([m[1] for m in mats], ctypes.c_int64),
+                  arr([m[2] for m in mats], ctypes.c_int64), arr([m[3] for m in mats], ctypes.c_int64),
+                  arr([m[4].data_ptr() for m in mats], ctypes.c_void_p), -1.0 / n_fit, _lib.stream(self.device))
+        for name in self.layout.names:
+            self.params[name].grad = grads[name].to(self.params[name].dtype)
         optimizer.step()
         self.last = dict(losses=losses, fitness=fitness, weight=weight)
         return losses.mean().item()

@@ -127,3 +127,23 @@ def test_dust_and_head_error_arguments_are_checked_before_any_gpu_call():
     d.sites = 4  # a block site without the captured input
     with pytest.raises(ValueError, match='captured input'):
         _lib.call('noise_dust_rerun', ctypes.byref(model), ctypes.byref(d), p, p, 2, 128, p, p, 1 << 30, None)
+
+
+def test_outer_grad_batch_arguments_are_checked_before_any_gpu_call():
+    """Every matrix is validated before the grouped launch: a slice past the noise row, a NULL gradient or a bad
+    shape anywhere in the list fails the call."""
+    import ctypes
+    from noise_amd import _lib
+    lib = _lib.lib()
+    arr = lambda vals, t: (t * len(vals))(*vals)
+    fake = ctypes.c_void_p(256)  # never dereferenced: the checks fail first
+
+    def call(a_off, b_off, out, n_in, grads, stride=100):
+        return lib.noise_outer_grad_batch(fake, stride, fake, 10, len(out), arr(a_off, ctypes.c_int64),
+                                          arr(b_off, ctypes.c_int64), arr(out, ctypes.c_int64), arr(n_in, ctypes.c_int64),
+                                          arr(grads, ctypes.c_void_p), 1.0, None)
+    assert call([0, 0], [10, 10], [10, 10], [10, 91], [256, 256]) == 1   # second slice ends past the 100-value row
+    assert 'matrix 1: slice beyond the noise row' in lib.noise_last_error().decode()
+    assert call([0], [10], [10], [10], [0]) == 1                         # NULL gradient
+    assert call([0], [10], [0], [10], [256]) == 1                        # empty matrix
+    assert call([-1], [10], [10], [10], [256]) == 1

@@ -44,6 +44,33 @@ def test_outer_grad_and_vector_grad(dev):
     _lib.call('noise_outer_grad', _lib.ptr(rows_d), stride, 3, -1, _lib.ptr(w_d), pairs, 1, 8, 2.0,
               _lib.ptr(vec), _lib.stream(dev))
     assert torch.allclose(vec.cpu(), 2.0 * (w @ rows[:, 3:11]), rtol=1e-4, atol=1e-4)
+    vec21 = torch.empty(21, device=dev)  # three 8-element blocks, the last partial
+    _lib.call('noise_outer_grad', _lib.ptr(rows_d), stride, 17, -1, _lib.ptr(w_d), pairs, 1, 21, -1.5,
+              _lib.ptr(vec21), _lib.stream(dev))
+    assert torch.allclose(vec21.cpu(), -1.5 * (w @ rows[:, 17:38]), rtol=1e-4, atol=1e-4)
+
+
+def test_outer_grad_batch(dev):
+    """Several matrices in one grouped launch: unaligned slice offsets, sizes that are not multiples of the 128 x 128
+    tile or of 4, a pair count that is not a multiple of the 16-pair stage, a matrix smaller than one tile and one
+    spanning many; each against its float64 outer-product sum."""
+    from noise_amd import _lib
+    import ctypes
+    g = torch.Generator().manual_seed(3)
+    pairs, stride = 333, 2100
+    rows = torch.randn(pairs, stride, generator=g)
+    w = torch.randn(pairs, generator=g)
+    mats = [(5, 300, 8, 32), (41, 700, 130, 70), (1, 2, 512, 513), (777, 1290, 257, 129)]  # a_off, b_off, out, in
+    grads = [torch.full((o, i), float('nan'), device=dev) for _, _, o, i in mats]
+    rows_d, w_d = rows.to(dev), w.to(dev)
+    arr = lambda vals, t: (t * len(vals))(*vals)
+    _lib.call('noise_outer_grad_batch', _lib.ptr(rows_d), stride, _lib.ptr(w_d), pairs, len(mats),
+              arr([m[0] for m in mats], ctypes.c_int64), arr([m[1] for m in mats], ctypes.c_int64),
+              arr([m[2] for m in mats], ctypes.c_int64), arr([m[3] for m in mats], ctypes.c_int64),
+              arr([t.data_ptr() for t in grads], ctypes.c_void_p), 0.5, _lib.stream(dev))
+    for (a0, b0, o, i), got in zip(mats, grads):
+        want = 0.5 * (w[:, None] * rows[:, a0:a0 + o]).t().double() @ rows[:, b0:b0 + i].double()
+        assert torch.allclose(got.cpu().double(), want, rtol=1e-4, atol=1e-4), (o, i)
 
 
 def test_adamw_matches_torch(dev):
