@@ -53,10 +53,22 @@ struct Jitter {
 
 // ---------------------------------------------------------------------------------------------------------------
 // x0 = norm(wte[tok] + sign a[tok] b [+ the direct draws' jitter])  (eggroll.py:61-63, 74; dust.py:218-220); 8 rows
-// per wave, 8 channels per lane.
+// per wave, 8 channels per lane. The kernel also forms block 0's input (eggroll.py:77-79, the work mix_norm_kernel does
+// for a later first block): x = (l_r + s eps_r) x0 + (l_0 + s eps_0) x0, h = norm(x) in bf16 and the three q/k/v dots
+// h . b. x0 itself is written only when asked: a capture, or later mixes that read it instead of recomputing it.
+struct EmbedMix {
+  float* x;
+  bf16_t* h;
+  float* xb;  // [M, 4]
+  const float* resid_lambdas;
+  const float* x0_lambdas;
+  int64_t off_resid, off_x0, off_b[3];
+  int write_x0;
+};
+
 __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __restrict__ wte, int Vp, int64_t off_wte,
                                                     Jitter jit, float* __restrict__ x0, float* __restrict__ x0_inv,
-                                                    int64_t M) {
+                                                    EmbedMix em, int64_t M) {
   // 8 consecutive rows per wave (M and the member length are multiples of 8, so they belong to one member): lanes
   // 0..7 fetch the rows' tokens and noise scalars together, the member's b vector is read once, and the 8 embedding
   // rows are loaded before any is reduced, so the dependent loads (member table, token, embedding row) overlap.
@@ -109,9 +121,58 @@ __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __r
   for (int q = 0; q < 8; ++q) {
     const float inv = lane_val(bad, q) ? __builtin_nanf("") : rsq_norm(lane_val(tot, 8 * q) * (1.0f / kD) + kNormEps);
     if (lane == q) x0_inv[r0 + q] = inv;
-    float* dst = x0 + (r0 + q) * kD + c0;
-    *(f32x4*)dst = f32x4{e[q][0] * inv, e[q][1] * inv, e[q][2] * inv, e[q][3] * inv};
-    *(f32x4*)(dst + 4) = f32x4{e[q][4] * inv, e[q][5] * inv, e[q][6] * inv, e[q][7] * inv};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[q][j] *= inv;  // x0
+    if (em.write_x0) {
+      float* dst = x0 + (r0 + q) * kD + c0;
+      *(f32x4*)dst = f32x4{e[q][0], e[q][1], e[q][2], e[q][3]};
+      *(f32x4*)(dst + 4) = f32x4{e[q][4], e[q][5], e[q][6], e[q][7]};
+    }
+  }
+  {
+    float lr = em.resid_lambdas[0], l0 = em.x0_lambdas[0];
+    if (nr) { lr += s * nr[em.off_resid]; l0 += s * nr[em.off_x0]; }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[q][j] = lr * e[q][j] + l0 * e[q][j];  // x
+      float* dst = em.x + (r0 + q) * kD + c0;
+      *(f32x4*)dst = f32x4{e[q][0], e[q][1], e[q][2], e[q][3]};
+      *(f32x4*)(dst + 4) = f32x4{e[q][4], e[q][5], e[q][6], e[q][7]};
+      ss[q] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss[q] += e[q][j] * e[q][j];
+    }
+    const float tot2 = warp_sum8(ss, lane);
+    float d[3][8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float inv = rsq_norm(lane_val(tot2, 8 * q) * (1.0f / kD) + kNormEps);
+      u32x4 packed;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) packed[j] = pack_bf16x2(e[q][2 * j] * inv, e[q][2 * j + 1] * inv);
+      *(u32x4*)(em.h + (r0 + q) * kD + c0) = packed;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { e[q][2 * j] = bf16_lo(packed[j]); e[q][2 * j + 1] = bf16_hi(packed[j]); }  // h
+#pragma unroll
+      for (int k = 0; k < 3; ++k) d[k][q] = 0.f;
+    }
+    if (nr) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const f32x4 b0 = *(const f32x4*)(nr + em.off_b[k] + c0), b1 = *(const f32x4*)(nr + em.off_b[k] + c0 + 4);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[k][q] += e[q][j] * b0[j] + e[q][4 + j] * b1[j];
+        }
+        const float dt = warp_sum8(d[k], lane);
+        if ((lane & 7) == 0) em.xb[(r0 + (lane >> 3)) * 4 + k] = dt;
+      }
+    } else if (lane < 8) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) em.xb[(r0 + lane) * 4 + k] = 0.f;
+    }
   }
 }
 
@@ -869,8 +930,15 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
     NOISE_LAUNCH_CHECK();
   } else {
     NoiseTimer tm(kTimeEmbed, stream);
+    EmbedMix em;
+    memset(&em, 0, sizeof(em));
+    em.x = ws.x; em.h = ws.h; em.xb = ws.xb;
+    em.resid_lambdas = model->resid_lambdas; em.x0_lambdas = model->x0_lambdas;
+    em.off_resid = pert->resid_lambdas; em.off_x0 = pert->x0_lambdas;
+    em.off_b[0] = pert->c_q[0] + kD; em.off_b[1] = pert->c_k[0] + kD; em.off_b[2] = pert->c_v[0] + kD;
+    em.write_x0 = dr->capture != nullptr || !x0_recompute;
     hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte,
-                       dr->jit(-1, 0), ws.x0, ws.x0_inv, M);
+                       dr->jit(-1, 0), ws.x0, ws.x0_inv, em, M);
     NOISE_LAUNCH_CHECK();
   }
   if (dr->capture)
@@ -882,12 +950,12 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
     NOISE_REQUIRE(L.w_qkv && L.w_proj && L.w_fc && L.w_mlp_proj, "layer %d weight pointer is NULL", i);
     NOISE_REQUIRE((L.w_gate == nullptr) == (L.ve == nullptr), "layer %d: w_gate and ve must both be set or both NULL", i);
     NOISE_REQUIRE(L.window >= 0, "layer %d: negative window", i);
-    if (i == first_layer) {
-      // lambda mix + norm + q/k/v dots + gate of the first block (later blocks get theirs from the epilogue of the
-      // previous block's MLP projection); a rerun from a captured block input starts from the mixed x: norm only
+    if (i == first_layer && from_block) {
+      // a rerun from a captured block input starts from the mixed x: norm, q/k/v dots and gate (block 0's come from
+      // the embedding kernel, later blocks' from the epilogue of the previous block's MLP projection)
       NormArgs na;
       memset(&na, 0, sizeof(na));
-      na.x = ws.x; na.x0 = ws.x0; na.mix = from_block ? 0 : 1; na.first = from_block ? 0 : 1;
+      na.x = ws.x; na.x0 = ws.x0; na.mix = 0; na.first = 0;
       na.resid_lambdas = model->resid_lambdas; na.x0_lambdas = model->x0_lambdas; na.layer = 0;
       na.off_resid = pert->resid_lambdas; na.off_x0 = pert->x0_lambdas;
       na.h = ws.h; na.ndot = 3;
@@ -896,7 +964,7 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
       NoiseTimer tm(kTimeNorm, stream);
       hipLaunchKernelGGL(mix_norm_kernel, dim3(row_blocks), dim3(256), 0, stream, mb, na);
       NOISE_LAUNCH_CHECK();
-    } else if (L.w_gate) {
+    } else if (L.w_gate) {  // the value-embedding gate from h
       NoiseTimer tm(kTimeNorm, stream);
       hipLaunchKernelGGL(gate_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), 0, stream, mb, ws.h, L.w_gate,
                          pert->ve_gate[i], ws.gate, M);
