@@ -761,7 +761,7 @@ __global__ __launch_bounds__(256) void member_sum_kernel(const float* __restrict
 
 using Tile = GemmShape<128, 256, 32, 2, 2, 3, 2>;  // two workgroups per CU: one's epilogue beside the other's MFMAs
 using RowTile = GemmShape<128, 512, 32, 2, 4>;     // whole 512-wide rows, for the epilogues that normalize
-constexpr int kAttnOG = 1;  // 32 outputs per wave (2 waves per SIMD)
+constexpr int kAttnOG = 1;  // 32 outputs per wave (4 waves per SIMD)
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 

@@ -73,6 +73,27 @@ def test_outer_grad_batch(dev):
         assert torch.allclose(got.cpu().double(), want, rtol=1e-4, atol=1e-4), (o, i)
 
 
+def test_outer_grad_batch_over_several_launches(dev):
+    """70 small matrices: more than one launch's 64-job table, so the entry point splits the list."""
+    from noise_amd import _lib
+    import ctypes
+    g = torch.Generator().manual_seed(4)
+    pairs, stride = 40, 400
+    rows = torch.randn(pairs, stride, generator=g)
+    w = torch.randn(pairs, generator=g)
+    mats = [(k, 200 + 2 * k, 3 + k % 5, 1 + k % 7) for k in range(70)]
+    grads = [torch.full((o, i), float('nan'), device=dev) for _, _, o, i in mats]
+    rows_d, w_d = rows.to(dev), w.to(dev)
+    arr = lambda vals, t: (t * len(vals))(*vals)
+    _lib.call('noise_outer_grad_batch', _lib.ptr(rows_d), stride, _lib.ptr(w_d), pairs, len(mats),
+              arr([m[0] for m in mats], ctypes.c_int64), arr([m[1] for m in mats], ctypes.c_int64),
+              arr([m[2] for m in mats], ctypes.c_int64), arr([m[3] for m in mats], ctypes.c_int64),
+              arr([t.data_ptr() for t in grads], ctypes.c_void_p), 1.0, _lib.stream(dev))
+    for (a0, b0, o, i), got in zip(mats, grads):
+        want = (w[:, None] * rows[:, a0:a0 + o]).t().double() @ rows[:, b0:b0 + i].double()
+        assert torch.allclose(got.cpu().double(), want, rtol=1e-4, atol=1e-4), (a0, o, i)
+
+
 def test_adamw_matches_torch(dev):
     from noise_amd.optim import AdamW
     g = torch.Generator().manual_seed(2)
