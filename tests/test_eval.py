@@ -76,3 +76,15 @@ def test_head_error_takes_device_tensors_only():
     with pytest.raises(ValueError):
         dust.head_error(raw, torch.zeros(1, 4, dtype=torch.long), torch.zeros(1, 4), draws=16)
     assert dust.chunk_size(48, 16) == 16 and dust.chunk_size(24, 16) == 12 and dust.chunk_size(7, 16) == 7
+
+
+def test_training_run_checks_its_arguments_first(tmp_path):
+    """Pairs that do not split into whole chunks, too few rows for one update, or a used output directory fail before
+    any GPU work."""
+    import torch
+    from noise_amd.train import train
+    rows = torch.zeros(16, 2049, dtype=torch.int64)
+    with pytest.raises(ValueError, match='whole chunks'):
+        train(output=tmp_path / 'o', pairs=100, rows=rows)
+    with pytest.raises(ValueError, match='no update'):
+        train(output=tmp_path / 'o', pairs=256, rows=rows[:7])

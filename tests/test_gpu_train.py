@@ -1,0 +1,39 @@
+"""The EGGROLL training run (archive/10M/train/val/eggroll.py:171-250) end to end on synthetic token rows: the files it
+writes, the final state dict loading strictly, the result's validation loss, and the run repeating bit for bit from
+the seed (the warmup update is undone by the rebuild)."""
+import json
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _rows(n, seed):
+    return torch.randint(0, 4096, (n, 2049), generator=torch.Generator().manual_seed(seed))
+
+
+def test_training_run_writes_its_files_and_repeats(dev, tmp_path):
+    from noise_amd import eval as ev
+    from noise_amd.train import BATCH, train
+    print('training run: 2 updates of 256 pairs, twice', flush=True)
+    rows, val = _rows(3 * BATCH, 5), _rows(4, 6)
+    out = [tmp_path / 'a', tmp_path / 'b']
+    res = [train(output=o, steps=2, eval_every=1, pairs=256, rows=rows, val_rows=val, log=lambda s: None) for o in out]
+    cfg = json.loads((out[0] / 'config.json').read_text())
+    assert cfg['steps'] == 2 and cfg['pairs'] == 256 and cfg['batch'] == BATCH
+    lines = [json.loads(l) for l in (out[0] / 'metrics.jsonl').read_text().splitlines()]
+    assert [l['step'] for l in lines] == [1, 2]
+    assert 'val_loss' in lines[0] and 'val_loss' not in lines[1]  # untimed validation every update but the last
+    assert all(8.0 < l['population_loss'] < 9.0 for l in lines)  # near ln 4096 at initialization
+    assert res[0]['steps'] == 2 and res[0]['tokens'] == 2 * BATCH * 2048
+    assert json.loads((out[0] / 'result.json').read_text()) == res[0]
+    state = torch.load(out[0] / 'final.pt', map_location='cpu', weights_only=True)
+    assert res[0]['val_loss'] == pytest.approx(ev.evaluate(state, rows=val), rel=1e-6)
+    # the same seed, the same run: losses and final weights bit for bit
+    lines_b = [json.loads(l) for l in (out[1] / 'metrics.jsonl').read_text().splitlines()]
+    assert [l['population_loss'] for l in lines] == [l['population_loss'] for l in lines_b]
+    state_b = torch.load(out[1] / 'final.pt', map_location='cpu', weights_only=True)
+    assert all(torch.equal(state[k], state_b[k]) for k in state)
+    init = {k: v.cpu() for k, v in __import__('noise_amd.train', fromlist=['make_model']).make_model(dev).state_dict().items()}
+    assert any(not torch.equal(state[k], init[k]) for k in state)  # the updates moved the weights
