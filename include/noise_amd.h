@@ -145,6 +145,19 @@ int noise_outer_grad_batch(const float* rows, int64_t stride, const float* weigh
                            const int64_t* a_off, const int64_t* b_off, const int64_t* out, const int64_t* in,
                            float* const* grads, float scale, void* stream);
 
+/* Dust's local linear map from a site's output error to its weight error (reassemble):
+ * grad[o, i] = scale * sum_t error[t * error_ld + o] * x[t * x_ld + i] for t < tokens, o < d_out, i < d_in; x is fp32,
+ * or bf16 with x_bf16 != 0 (the captured bf16 site inputs). fp32 products and sums (fp32 MFMA).
+ * Replaces: train/val/dust.py:386-392 and train/val/run.py:861-867 (einsum 'btd,bti->di'). */
+int noise_reassemble(const float* error, int64_t error_ld, const void* x, int32_t x_bf16, int64_t x_ld, int64_t tokens,
+                     int64_t d_out, int64_t d_in, float scale, float* grad, void* stream);
+
+/* The embedding case: grad[v, :] = sum of error[t, :] over the tokens t with ids[t] == v, for v < vocab (every row is
+ * written; ids outside [0, vocab) contribute nothing). Deterministic (a fixed order per row).
+ * Replaces: train/val/dust.py:389-391, train/val/run.py:864-866 (index_add_ over the token ids). */
+int noise_reassemble_embedding(const float* error, int64_t error_ld, const int64_t* ids, int64_t tokens, int64_t vocab,
+                               int64_t width, float* grad, void* stream);
+
 /* One AdamW step on n fp32 elements in place (torch.optim.AdamW arithmetic): p *= 1 - lr wd; m = lerp(m, g, 1-b1);
  * v = b2 v + (1 - b2) g^2; p -= lr / (1 - b1^step) * m / (sqrt(v) / sqrt(1 - b2^step) + eps).
  * shadow (optional): bf16 copy of the updated p. Replaces: archive/10M/train/val/eggroll.py:205, 167 and
@@ -199,6 +212,16 @@ typedef struct noise_dust_draws {
 int noise_dust_capture(const noise_gpt* model, const int64_t* tokens, const int64_t* targets, int64_t n_seq,
                        int64_t T, float* token_loss, float* capture, void* workspace, size_t workspace_bytes,
                        void* stream);
+
+/* noise_dust_capture that also keeps, per block, the inputs of the writers' linears (each pointer may be NULL):
+ * attn_in [n_layer, n_seq * T, 512] bf16 attn.c_proj's input (the attention output); fc_in [n_layer, n_seq * T, 512]
+ * fp32 mlp.c_fc's input (the MLP's RMS-normed input); mlp_in [n_layer, n_seq * T, 2048] bf16 mlp.c_proj's input
+ * (relu² of c_fc). They hold the values the reference's hooks cache (the bf16 activations are exact in bf16), and are
+ * what noise_reassemble multiplies a site's output error by.
+ * Replaces: train/val/dust.py:139-179 (the forward hooks caching every Linear's input, self.inputs). */
+int noise_dust_capture_sites(const noise_gpt* model, const int64_t* tokens, const int64_t* targets, int64_t n_seq,
+                             int64_t T, float* token_loss, float* capture, uint16_t* attn_in, float* fc_in,
+                             uint16_t* mlp_in, void* workspace, size_t workspace_bytes, void* stream);
 /* Per-token CE of the chunk's draws, token_loss fp32 [n_draws, n_seq, T], clean weights.
  * Workspace: noise_dust_workspace(n_draws, n_seq, T).
  * Replaces: train/val/dust.py:210-233 (DUST.rerun with block_forward's jitter sites, :104-120, and head_loss,

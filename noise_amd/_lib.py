@@ -57,6 +57,8 @@ _SIGNATURES = {
     'noise_fitness': ([c_p, i64, i64, c_p, c_p, c_p], ctypes.c_int),
     'noise_outer_grad': ([c_p, i64, i64, i64, c_p, i64, i64, i64, f32, c_p, c_p], ctypes.c_int),
     'noise_outer_grad_batch': ([c_p, i64, c_p, i64, ctypes.c_int32, c_p, c_p, c_p, c_p, c_p, f32, c_p], ctypes.c_int),
+    'noise_reassemble': ([c_p, i64, c_p, i32, i64, i64, i64, i64, f32, c_p, c_p], ctypes.c_int),
+    'noise_reassemble_embedding': ([c_p, i64, c_p, i64, i64, i64, c_p, c_p], ctypes.c_int),
     'noise_adamw': ([c_p, c_p, c_p, c_p, i64, f32, f32, f32, f32, f32, i64, c_p, c_p], ctypes.c_int),
     'noise_credit_lse': ([c_p, c_p, i64, i64, i32, c_p, c_p], ctypes.c_int),
     'noise_credit_value': ([c_p, c_p, c_p, c_p, i64, i64, i32, i32, c_p, c_p], ctypes.c_int),
@@ -64,6 +66,8 @@ _SIGNATURES = {
     'noise_head_error': ([c_p, i64, c_p, c_p, i32, i32, i32, i32, i32, f32, u64, c_p, c_p, szt, c_p], ctypes.c_int),
     'noise_head_error_workspace': ([i64, i32, i32], szt),
     'noise_dust_capture': ([ctypes.POINTER(NoiseGpt), c_p, c_p, i64, i64, c_p, c_p, c_p, szt, c_p], ctypes.c_int),
+    'noise_dust_capture_sites': ([ctypes.POINTER(NoiseGpt), c_p, c_p, i64, i64, c_p, c_p, c_p, c_p, c_p, c_p, szt, c_p],
+                                 ctypes.c_int),
     'noise_dust_rerun': ([ctypes.POINTER(NoiseGpt), ctypes.POINTER(NoiseDustDraws), c_p, c_p, i64, i64, c_p, c_p, szt,
                           c_p], ctypes.c_int),
     'noise_dust_workspace': ([i64, i64, i64], szt),

@@ -816,6 +816,21 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict
   rope[i] = u32x4{pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3]), pack_bf16x2(sn[0], sn[1]), pack_bf16x2(sn[2], sn[3])};
 }
 
+// dst[r] = norm(src[r]) in fp32, one wave per row (the MLP's input as the capture keeps it)
+__global__ __launch_bounds__(256) void rms_rows_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                       int64_t M) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= M) return;
+  const int c0 = (threadIdx.x & 63) * 8;
+  const f32x4 v0 = *(const f32x4*)(src + r * kD + c0), v1 = *(const f32x4*)(src + r * kD + c0 + 4);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ss += v0[j] * v0[j] + v1[j] * v1[j];
+  const float inv = rsq_norm(warp_sum(ss) * (1.0f / kD) + kNormEps);
+  *(f32x4*)(dst + r * kD + c0) = f32x4{v0[0] * inv, v0[1] * inv, v0[2] * inv, v0[3] * inv};
+  *(f32x4*)(dst + r * kD + c0 + 4) = f32x4{v1[0] * inv, v1[1] * inv, v1[2] * inv, v1[3] * inv};
+}
+
 // dst[r] = src[the member's batch row, same position]: the captured block input replicated over the draws
 __global__ __launch_bounds__(256) void replicate_rows_kernel(Members mb, const float* __restrict__ src,
                                                              float* __restrict__ dst, int64_t M) {
@@ -871,6 +886,10 @@ struct DustRun {
   uint64_t seed;
   int draw0, n_seq;
   float* capture;  // [n_layer + 1, M, 512]: block inputs, then x0
+  // optional, [n_layer, M, width] bf16: the inputs of the writers' linears, for reassembling weight errors
+  bf16_t* cap_attn;  // attn.c_proj's input (the attention output), width 512
+  float* cap_fc;     // mlp.c_fc's input (the MLP's normed input, fp32 as the reference's F.rms_norm gives it), 512
+  bf16_t* cap_mlp;   // mlp.c_proj's input (relu² of c_fc), width 2048
   // the jitter of site s when it is set and block i is the entry
   Jitter jit(int i, int s) const {
     Jitter j;
@@ -1000,6 +1019,9 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
       NoiseTimer tm(kTimeAttention, stream);
       NOISE_CHECK_HIP((launch_flash<kAttn, true, kAttnOG>(fa, members, kH, stream)));
     }
+    if (dr->cap_attn)
+      NOISE_CHECK_HIP(hipMemcpyAsync(dr->cap_attn + (int64_t)i * M * kD, ws.y, (size_t)M * kD * 2,
+                                     hipMemcpyDeviceToDevice, stream));
 
     // attention projection + residual, then the MLP's norm and c_fc's rank-1 dot
     EpiResidNorm<false, 1> ep;
@@ -1020,6 +1042,11 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
       }
     }
 
+    if (dr->cap_fc) {
+      hipLaunchKernelGGL(rms_rows_kernel, dim3(row_blocks), dim3(256), 0, stream, ws.x, dr->cap_fc + (int64_t)i * M * kD,
+                         M);
+      NOISE_LAUNCH_CHECK();
+    }
     {
       NoiseTimer tm(kTimeFc, stream);
       const Jitter jf = dr->jit(i, 3);
@@ -1031,6 +1058,10 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
         NOISE_CHECK_HIP((launch_gemm<Tile>(ws.h, kD, L.w_fc, kD, (int)M, kF, kD, er, stream)));
       }
     }
+
+    if (dr->cap_mlp)
+      NOISE_CHECK_HIP(hipMemcpyAsync(dr->cap_mlp + (int64_t)i * M * kF, ws.hid, (size_t)M * kF * 2,
+                                     hipMemcpyDeviceToDevice, stream));
 
     // MLP projection + residual, then the next block's lambda mix, norm and q/k/v dots (or the final norm and
     // lm_head's rank-1 dot)
@@ -1137,15 +1168,24 @@ static int dust_forward(const noise_gpt* model, const int64_t* tokens, const int
                       token_loss, nullptr, (char*)workspace + head, workspace_bytes - head, stream, &dr);
 }
 
-extern "C" int noise_dust_capture(const noise_gpt* model, const int64_t* tokens, const int64_t* targets, int64_t n_seq,
-                                  int64_t T, float* token_loss, float* capture, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
+extern "C" int noise_dust_capture_sites(const noise_gpt* model, const int64_t* tokens, const int64_t* targets,
+                                        int64_t n_seq, int64_t T, float* token_loss, float* capture,
+                                        uint16_t* attn_in, float* fc_in, uint16_t* mlp_in, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
   NOISE_REQUIRE(capture, "capture is NULL");
   DustRun dr;
   memset(&dr, 0, sizeof(dr));
   dr.entry = -1; dr.n_seq = (int)n_seq; dr.capture = capture;
+  dr.cap_attn = (bf16_t*)attn_in; dr.cap_fc = fc_in; dr.cap_mlp = (bf16_t*)mlp_in;
   return dust_forward(model, tokens, targets, n_seq, T, 1, token_loss, workspace, workspace_bytes,
                       (hipStream_t)stream, dr);
+}
+
+extern "C" int noise_dust_capture(const noise_gpt* model, const int64_t* tokens, const int64_t* targets, int64_t n_seq,
+                                  int64_t T, float* token_loss, float* capture, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  return noise_dust_capture_sites(model, tokens, targets, n_seq, T, token_loss, capture, nullptr, nullptr, nullptr,
+                                  workspace, workspace_bytes, stream);
 }
 
 extern "C" int noise_dust_rerun(const noise_gpt* model, const noise_dust_draws* d, const int64_t* tokens,

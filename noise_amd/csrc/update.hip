@@ -61,7 +61,7 @@ __global__ __launch_bounds__(1024) void fitness_kernel(const float* __restrict__
 constexpr int kOgTile = 128, kOgK = 16, kOgPitch = 160, kOgMaxJobs = 64;
 
 struct OgJob {
-  int64_t a_off, b_off;  // slice offsets of a (out values) and b (in values) in a noise row
+  int64_t a_off, b_off;  // column offsets of a (out values) and b (in values) in their rows
   int32_t out, in;
   int32_t tile0, n_in_tiles;
   float* grad;           // [out, in]
@@ -71,7 +71,10 @@ struct OgJobs {
   OgJob job[kOgMaxJobs];
 };
 
-__global__ __launch_bounds__(256) void outer_grad_kernel(const float* __restrict__ rows, int64_t stride,
+// Sum over k < n_k of a_k b_k^T with row k of A at a_rows + k a_stride (fp32) and of B at b_rows + k b_stride (fp32,
+// or bf16 with b_bf16), b_k scaled by weight[k] when a weight is given.
+__global__ __launch_bounds__(256) void outer_grad_kernel(const float* __restrict__ a_rows, int64_t a_stride,
+                                                         const void* __restrict__ b_rows, int64_t b_stride, int b_bf16,
                                                          const float* __restrict__ weight, int64_t pairs, float scale,
                                                          OgJobs jobs) {
   __shared__ float as[2][kOgK][kOgPitch];
@@ -94,9 +97,15 @@ __global__ __launch_bounds__(256) void outer_grad_kernel(const float* __restrict
     for (int q = 0; q < 8; ++q) {
       const int64_t j = j0 + row0 + 2 * q;
       const bool live = j < pairs;
-      const float* row = rows + (live ? j : 0) * stride;
-      ra[q] = (live && a_in) ? row[a_off + o0 + col] : 0.f;
-      rb[q] = (live && b_in) ? weight[j] * row[b_off + i0 + col] : 0.f;
+      const int64_t jj = live ? j : 0;
+      ra[q] = (live && a_in) ? a_rows[jj * a_stride + a_off + o0 + col] : 0.f;
+      float bv = 0.f;
+      if (live && b_in) {
+        const int64_t at = jj * b_stride + b_off + i0 + col;
+        bv = b_bf16 ? bf16_to_f32(((const bf16_t*)b_rows)[at]) : ((const float*)b_rows)[at];
+        if (weight) bv = weight[j] * bv;
+      }
+      rb[q] = bv;
     }
   };
   auto store = [&](int st) {
@@ -268,9 +277,79 @@ extern "C" int noise_outer_grad_batch(const float* rows, int64_t stride, const f
     }
     if (tiles == 0) continue;
     hipLaunchKernelGGL(outer_grad_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, rows, stride,
-                       weight, pairs, scale, jobs);
+                       (const void*)rows, stride, 0, weight, pairs, scale, jobs);
     NOISE_LAUNCH_CHECK();
   }
+  return NOISE_OK;
+}
+
+// weight_error[o, i] = scale sum_t error[t, o] x[t, i] (train/val/dust.py:386-392, run.py:861-867, the einsum
+// 'btd,bti->di'), on the grouped outer-product kernel with one job, the tokens as its K.
+extern "C" int noise_reassemble(const float* error, int64_t error_ld, const void* x, int32_t x_bf16, int64_t x_ld,
+                                int64_t tokens, int64_t d_out, int64_t d_in, float scale, float* grad, void* stream) {
+  NOISE_REQUIRE(error && x && grad, "NULL pointer argument");
+  NOISE_REQUIRE(tokens > 0 && d_out > 0 && d_in > 0 && d_out <= INT32_MAX && d_in <= INT32_MAX, "bad sizes");
+  NOISE_REQUIRE(error_ld >= d_out && x_ld >= d_in, "row strides shorter than the rows");
+  OgJobs jobs;
+  memset(&jobs, 0, sizeof(jobs));
+  jobs.n = 1;
+  OgJob& g = jobs.job[0];
+  g.out = (int32_t)d_out; g.in = (int32_t)d_in; g.grad = grad;
+  g.n_in_tiles = (int32_t)((d_in + kOgTile - 1) / kOgTile);
+  const int64_t tiles = (int64_t)g.n_in_tiles * ((d_out + kOgTile - 1) / kOgTile);
+  NOISE_REQUIRE(tiles <= INT32_MAX, "too many tiles");
+  NoiseTimer tm(kTimeUpdate, (hipStream_t)stream);
+  hipLaunchKernelGGL(outer_grad_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, error, error_ld, x,
+                     x_ld, x_bf16 ? 1 : 0, (const float*)nullptr, tokens, scale, jobs);
+  NOISE_LAUNCH_CHECK();
+  return NOISE_OK;
+}
+
+// weight_error[v, :] = sum over the tokens t with ids[t] == v of error[t, :] (the embedding case of reassemble:
+// index_add_ over the token ids). One workgroup per table row (and 512 columns) scans the ids 128 at a time: each
+// thread tests one id, the two waves' ballots go to LDS, and every thread then adds the matching error rows in
+// position order, 4 columns a thread. The order is fixed, so the sums are deterministic. Other ids add nothing.
+__global__ __launch_bounds__(128) void scatter_rows_kernel(const float* __restrict__ error, int64_t error_ld,
+                                                           const int64_t* __restrict__ ids, int64_t tokens,
+                                                           int64_t width, float* __restrict__ grad) {
+  __shared__ uint64_t mask[2];
+  const int64_t v = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.y * 512 + tid * 4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t t0 = 0; t0 < tokens; t0 += 128) {
+    const int64_t t = t0 + tid;
+    const uint64_t b = __ballot(t < tokens && ids[t] == v);
+    if ((tid & 63) == 0) mask[tid >> 6] = b;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      uint64_t mk = mask[w];
+      while (mk) {
+        const int k = __builtin_ctzll(mk);
+        mk &= mk - 1;
+        const float* row = error + (t0 + 64 * w + k) * error_ld;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (c0 + e < width) acc[e] += row[c0 + e];
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (c0 + e < width) grad[v * width + c0 + e] = acc[e];
+}
+
+extern "C" int noise_reassemble_embedding(const float* error, int64_t error_ld, const int64_t* ids, int64_t tokens,
+                                          int64_t vocab, int64_t width, float* grad, void* stream) {
+  NOISE_REQUIRE(error && ids && grad, "NULL pointer argument");
+  NOISE_REQUIRE(tokens > 0 && vocab > 0 && width > 0 && error_ld >= width, "bad sizes");
+  NOISE_REQUIRE(vocab <= INT32_MAX && (width + 511) / 512 <= 65535, "table too large");
+  NoiseTimer tm(kTimeUpdate, (hipStream_t)stream);
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)vocab, (unsigned)((width + 511) / 512)), dim3(128), 0,
+                     (hipStream_t)stream, error, error_ld, ids, tokens, width, grad);
+  NOISE_LAUNCH_CHECK();
   return NOISE_OK;
 }
 

@@ -74,9 +74,10 @@ def parse_site(model, name):
 class Dust:
     """The direct-draw part of DUST (train/val/dust.py:131-259) over the HIP population forward.
 
-    capture(x, y) runs the clean pass, keeping every block's input and the clean per-token losses; rerun(n, entry,
-    sites, sigma, draw0) evaluates n jittered draws from block `entry` (None: from the token embedding);
-    direct_errors(sites, draws, sigma, entry, gamma) returns the reference's error estimates. The jitter's draw counter
+    capture(x, y) runs the clean pass, keeping every block's input, the inputs of the writers' linears and the clean
+    per-token losses; rerun(n, entry, sites, sigma, draw0) evaluates n jittered draws from block `entry` (None: from
+    the token embedding); direct_errors(sites, draws, sigma, entry, gamma) returns the reference's error estimates, and
+    reassemble(site, error) turns a site's output error into its weight error (dust.py:386-392). The jitter's draw counter
     advances like the reference's generator, so successive calls use fresh draws; `seed` and `rank` key the stream as
     the reference keys its generator (dust.py:149)."""
 
@@ -102,10 +103,21 @@ class Dust:
         self.batch, self.length = b, T
         L, D = model.config.n_layer, model.config.n_embd
         self.blocks = torch.empty(L + 1, b, T, D, dtype=torch.float32, device=dev)
+        F = 4 * D
+        attn_in = torch.empty(L, b, T, D, dtype=torch.bfloat16, device=dev)
+        fc_in = torch.empty(L, b, T, D, dtype=torch.float32, device=dev)
+        mlp_in = torch.empty(L, b, T, F, dtype=torch.bfloat16, device=dev)
         loss = torch.empty(b, T, dtype=torch.float32, device=dev)
         ws = workspace(dev, _lib.lib().noise_dust_workspace(1, b, T))
-        _lib.call('noise_dust_capture', ctypes.byref(s), _lib.ptr(self.x), _lib.ptr(self.y), b, T, _lib.ptr(loss),
-                  _lib.ptr(self.blocks), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+        _lib.call('noise_dust_capture_sites', ctypes.byref(s), _lib.ptr(self.x), _lib.ptr(self.y), b, T, _lib.ptr(loss),
+                  _lib.ptr(self.blocks), _lib.ptr(attn_in), _lib.ptr(fc_in), _lib.ptr(mlp_in), _lib.ptr(ws), ws.numel(),
+                  _lib.stream(dev))
+        # the linears' inputs, by site name, as the reference's hooks keep them (dust.py:173-179)
+        self.inputs = {'transformer.wte': self.x}
+        for i in range(L):
+            self.inputs[SITES['attn'].format(i)] = attn_in[i]
+            self.inputs[SITES['fc'].format(i)] = fc_in[i]
+            self.inputs[SITES['mlp'].format(i)] = mlp_in[i]
         self.x0 = self.blocks[L]
         self.clean_loss = loss
         return loss
@@ -154,3 +166,28 @@ class Dust:
                           float(sigma), self.seed, draw0, sid, width, _lib.ptr(errors[name]), _lib.ptr(ws),
                           ws.numel(), _lib.stream(dev))
         return {s: e / draws for s, e in errors.items()}
+
+    def reassemble(self, site, error):
+        """The weight error of `site` from its output error (b, t, width) (dust.py:386-392): error times the captured
+        input, summed over the tokens, [out, in] fp32; for the token embedding, the error rows added into their
+        tokens' rows of a [padded vocab, 512] table."""
+        if site not in self.inputs:
+            raise KeyError(f'no linear input captured for site {site!r}')
+        x = self.inputs[site]
+        b, T = self.batch, self.length
+        error = error.float().contiguous()
+        if error.shape[:2] != (b, T):
+            raise ValueError(f'error {tuple(error.shape)} does not match the captured batch ({b}, {T})')
+        _lib.require_device(error)
+        width = error.shape[-1]
+        if site == 'transformer.wte':
+            Vp = self.model.transformer.wte.weight.shape[0]
+            out = torch.empty(Vp, width, dtype=torch.float32, device=error.device)
+            _lib.call('noise_reassemble_embedding', _lib.ptr(error), width, _lib.ptr(x), b * T, Vp, width,
+                      _lib.ptr(out), _lib.stream(error.device))
+            return out
+        d_in = x.shape[-1]
+        out = torch.empty(width, d_in, dtype=torch.float32, device=error.device)
+        _lib.call('noise_reassemble', _lib.ptr(error), width, _lib.ptr(x), int(x.dtype == torch.bfloat16), d_in, b * T,
+                  width, d_in, 1.0, _lib.ptr(out), _lib.stream(error.device))
+        return out

@@ -14,7 +14,9 @@ Stein's lemma, the estimate over many small-sigma draws against (1 - 1/b) times 
 soft-capped CE with respect to the raw logits. The direct draws: a rerun without jitter equals the clean per-token
 losses from every entry; reward_to_go against a brute-force double loop; by Stein's lemma, direct_errors over many
 draws against (1 - 1/n) times the autograd derivative of each token's loss with respect to that token's site
-activation (and, with gamma, the decayed sum over later tokens' losses).
+activation (and, with gamma, the decayed sum over later tokens' losses). reassemble (dust.py:386-392) against
+brute-force loops, a closed-form total and, for the embedding, conservation of the error rows; the captured linear
+inputs against the block arithmetic they feed (the next block's captured input rebuilt from them).
 """
 from __future__ import annotations
 
@@ -105,8 +107,9 @@ def dust_jitter(seed, draw, site, b, t, width):
     return torch.from_numpy(rng.dust_noise(seed, draw, SITE_ID[site], 0, b * t, width)).view(b, t, width)
 
 
-def block_forward(p, cfg, i, x, idx, cos, sin, jitter=None):
-    """Block i on its (mixed) input x with jitter added at o / attn / fc / mlp (dust.py:104-120)."""
+def block_forward(p, cfg, i, x, idx, cos, sin, jitter=None, inputs=None):
+    """Block i on its (mixed) input x with jitter added at o / attn / fc / mlp (dust.py:104-120). `inputs` (a dict)
+    receives the writers' linear inputs under 'attn', 'fc', 'mlp' (what dust.py:173-179's hooks cache)."""
     jitter = jitter or {}
     add = lambda v, key: v if key not in jitter else v + jitter[key]
     B, T, _ = x.shape
@@ -123,8 +126,12 @@ def block_forward(p, cfg, i, x, idx, cos, sin, jitter=None):
     q, k = om.rms_norm(om.apply_rotary(q, cos, sin)), om.rms_norm(om.apply_rotary(k, cos, sin))
     y = add(om.attention(q, k, v, om.window_sizes(cfg)[i]).reshape(B, T, -1), 'o')
     x = x + add(y @ p[pre + 'attn.c_proj.weight'].t(), 'attn')
-    hidden = add(om.rms_norm(x) @ p[pre + 'mlp.c_fc.weight'].t(), 'fc')
-    return x + add(torch.relu(hidden).square() @ p[pre + 'mlp.c_proj.weight'].t(), 'mlp')
+    h2 = om.rms_norm(x)
+    hidden = add(h2 @ p[pre + 'mlp.c_fc.weight'].t(), 'fc')
+    act = torch.relu(hidden).square()
+    if inputs is not None:
+        inputs.update(attn=y, fc=h2, mlp=act)
+    return x + add(act @ p[pre + 'mlp.c_proj.weight'].t(), 'mlp')
 
 
 def head_loss(p, cfg, x, targets):
@@ -133,17 +140,35 @@ def head_loss(p, cfg, x, targets):
     return om.softcap_ce(logits, targets)
 
 
-def capture(p, cfg, idx, targets):
-    """The clean pass: (blocks, x0, per-token losses [B, T]), blocks[i] = block i's mixed input (dust.py:195-208)."""
+def capture(p, cfg, idx, targets, inputs=None):
+    """The clean pass: (blocks, x0, per-token losses [B, T]), blocks[i] = block i's mixed input (dust.py:195-208).
+    `inputs` (a dict) receives every writer linear's input by site name, and the token ids under 'transformer.wte'."""
     B, T = idx.shape
     cos, sin = om.rotary(T, cfg.head_dim)
     x = x0 = om.rms_norm(p['transformer.wte.weight'][idx])
     blocks = []
+    if inputs is not None:
+        inputs['transformer.wte'] = idx
     for i in range(cfg.n_layer):
         x = p['resid_lambdas'][i] * x + p['x0_lambdas'][i] * x0
         blocks.append(x)
-        x = block_forward(p, cfg, i, x, idx, cos, sin)
+        got = {} if inputs is not None else None
+        x = block_forward(p, cfg, i, x, idx, cos, sin, inputs=got)
+        if inputs is not None:
+            for key, name in (('attn', 'attn.c_proj'), ('fc', 'mlp.c_fc'), ('mlp', 'mlp.c_proj')):
+                inputs[f'transformer.h.{i}.{name}'] = got[key]
     return blocks, x0, head_loss(p, cfg, x, targets)
+
+
+def reassemble(x, error, vocab=None):
+    """A site's weight error from its output error (dust.py:386-392): the embedding case (token ids x, a table of
+    `vocab` rows) adds each token's error row into its id's row (index_add_); a linear's is error^T x summed over the
+    tokens (einsum 'btd,bti->di')."""
+    error = error.double()
+    if vocab is not None:
+        return torch.zeros(vocab, error.shape[-1], dtype=torch.float64).index_add_(
+            0, x.reshape(-1), error.reshape(-1, error.shape[-1]))
+    return torch.einsum('btd,bti->di', error, x.double())
 
 
 def rerun(p, cfg, state, n, entry, sites, sigma, seed, draw0):

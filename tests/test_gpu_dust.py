@@ -132,3 +132,55 @@ def test_error_sums_match_oracle_on_the_same_losses(dev, gamma):
                   for c, d0 in zip(chunks, (0, 4))) / 8
         assert (((est[name].cpu() - ref).abs().max()) / ref.abs().max()).item() < 1e-4, name
     assert d.next_draw == 8
+
+
+def _oracle_inputs():
+    if 'inputs' not in _ST:
+        ocfg, w, st, _ = _ST['st']
+        inputs = {}
+        od.capture(w, ocfg, st['idx'], st['targets'], inputs=inputs)
+        _ST['inputs'] = inputs
+    return _ST['inputs']
+
+
+def test_capture_keeps_the_writers_inputs(dev):
+    """The capture's linear inputs (attention output, the MLP's normed input, relu² of c_fc; bf16 where the forward
+    holds bf16) against the oracle's fp32 ones."""
+    print('dust capture inputs B=2 T=256', flush=True)
+    from noise_amd.dust import Dust
+    ocfg, w, st, model = _setup(dev)
+    d = Dust(model)
+    d.capture(st['idx'].to(dev), st['targets'].to(dev))
+    ref = _oracle_inputs()
+    assert torch.equal(d.inputs['transformer.wte'].cpu(), st['idx'])
+    for name, want in ref.items():
+        if name == 'transformer.wte':
+            continue
+        got = d.inputs[name].float().cpu()
+        assert ((got - want).norm() / want.norm()).item() < 1e-2, name
+
+
+@pytest.mark.parametrize('site', ['transformer.h.1.attn.c_proj', 'transformer.h.1.mlp.c_fc',
+                                  'transformer.h.6.mlp.c_proj', 'transformer.wte'])
+def test_reassemble(dev, site):
+    """reassemble against a float64 einsum / index_add on the GPU's own captured input (the kernel's arithmetic, 1e-4
+    of the largest entry) and against the oracle's reassemble of its own input (1e-2 in norm)."""
+    print(f'dust reassemble {site}', flush=True)
+    from noise_amd.dust import Dust, parse_site
+    ocfg, w, st, model = _setup(dev)
+    d = Dust(model)
+    d.capture(st['idx'].to(dev), st['targets'].to(dev))
+    _, _, width = parse_site(model, site)
+    err = torch.randn(2, SEQ, width, generator=torch.Generator().manual_seed(len(site)))
+    got = d.reassemble(site, err.to(dev)).cpu().double()
+    x = d.inputs[site].cpu()
+    if site == 'transformer.wte':
+        vocab = model.transformer.wte.weight.shape[0]
+        exact = od.reassemble(x, err, vocab=vocab)
+        oracle = od.reassemble(_oracle_inputs()[site], err, vocab=vocab)
+    else:
+        exact = od.reassemble(x.float(), err)
+        oracle = od.reassemble(_oracle_inputs()[site], err)
+    assert got.shape == exact.shape
+    assert ((got - exact).abs().max() / exact.abs().max()).item() < 1e-4
+    assert ((got - oracle).norm() / oracle.norm()).item() < 1e-2

@@ -148,3 +148,57 @@ def test_direct_errors_tend_to_scaled_own_token_gradient():
     est = od.direct_errors(p, cfg, st, [site], draws=3072, sigma=0.02, entry=entry, nrep=2, seed=3)[site]
     slope = (est * g).sum() / (g * g).sum()
     assert 0.4 < slope.item() < 0.6, slope.item()
+
+
+# ---- reassemble (dust.py:386-392) and the captured linear inputs ----
+
+def test_reassemble_linear_against_brute_force_and_a_closed_form():
+    g = torch.Generator().manual_seed(21)
+    err, x = torch.randn(2, 3, 4, generator=g), torch.randn(2, 3, 5, generator=g)
+    got = od.reassemble(x, err)
+    want = torch.zeros(4, 5, dtype=torch.float64)
+    for b in range(2):
+        for t in range(3):
+            for d in range(4):
+                for i in range(5):
+                    want[d, i] += float(err[b, t, d]) * float(x[b, t, i])
+    assert torch.allclose(got, want, atol=1e-12)
+    # the total is the token sum of (sum of the error row) x (sum of the input row)
+    total = sum(float(err[b, t].double().sum()) * float(x[b, t].double().sum()) for b in range(2) for t in range(3))
+    assert abs(got.sum().item() - total) < 1e-9
+    planted = torch.einsum('btd,bti->id', err.double(), x.double())  # a transposed result
+    assert planted.shape != got.shape or not torch.allclose(planted, got)
+
+
+def test_reassemble_embedding_adds_each_token_row_into_its_id():
+    g = torch.Generator().manual_seed(22)
+    ids = torch.tensor([[3, 1, 3], [0, 3, 6]])
+    err = torch.randn(2, 3, 4, generator=g)
+    got = od.reassemble(ids, err, vocab=8)
+    want = torch.zeros(8, 4, dtype=torch.float64)
+    for b in range(2):
+        for t in range(3):
+            want[int(ids[b, t])] += err[b, t].double()
+    assert torch.allclose(got, want, atol=1e-12)
+    assert torch.allclose(got.sum(0), err.double().sum((0, 1)), atol=1e-12)  # every error row lands once
+    assert torch.count_nonzero(got.abs().sum(1)).item() == 4                 # ids 0, 1, 3, 6
+
+
+def test_captured_linear_inputs_rebuild_the_next_block_input():
+    """From block i's captured input and its captured linear inputs, the attention projection, the MLP's norm and the
+    MLP projection reproduce the next block's captured input: the inputs are the ones the forward used."""
+    cfg = om.Config(sequence_len=64)
+    w = recipe.weights(cfg, seed=5)
+    idx, tg = recipe.tokens(cfg, batch=1, seed=6)
+    inputs = {}
+    blocks, x0, _ = od.capture(w, cfg, idx, tg, inputs=inputs)
+    assert torch.equal(inputs['transformer.wte'], idx)
+    for i in range(cfg.n_layer - 1):
+        pre = f'transformer.h.{i}.'
+        x_attn = blocks[i] + inputs[pre + 'attn.c_proj'] @ w[pre + 'attn.c_proj.weight'].t()
+        assert torch.allclose(inputs[pre + 'mlp.c_fc'], om.rms_norm(x_attn), atol=1e-6)
+        act = torch.relu(inputs[pre + 'mlp.c_fc'] @ w[pre + 'mlp.c_fc.weight'].t()).square()
+        assert torch.allclose(inputs[pre + 'mlp.c_proj'], act, atol=1e-6)
+        x_out = x_attn + act @ w[pre + 'mlp.c_proj.weight'].t()
+        nxt = w['resid_lambdas'][i + 1] * x_out + w['x0_lambdas'][i + 1] * x0
+        assert torch.allclose(blocks[i + 1], nxt, atol=1e-5), i
