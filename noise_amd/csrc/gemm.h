@@ -329,7 +329,18 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   //   load(row0, n0, lane, const Wave&, Pre&)     the per-row data of one group (issued a group ahead),
   //   rows<R>(row0, n0, n_tile, lane, const Wave&, const Pre&, v)  the group's arithmetic and stores, with
   //   v = f32x4[R] (256-column tiles) or f32x4[R][2] (512-column tiles: columns 4l.. and 256 + 4l..).
+  // The wave's per-row loads and its first group's loads are issued before the accumulators are staged, so their
+  // memory latency runs behind the staging.
   bf16_t* st = (bf16_t*)smem_raw;
+  constexpr int R = Epi::kRows, G = S::kWaveRows / Epi::kRows, H = S::BN / 256;
+  static_assert(G % 2 == 0, "groups are processed in pairs");
+  const int row_base = m0 + wave * S::kWaveRows;
+  typename Epi::Wave w;
+  typename Epi::Pre p0, p1;
+  if (row_base < M) {
+    epi.begin(row_base, n0, lane, min(S::kWaveRows, M - row_base), w);  // per-row loads by lane: lanes < nrows
+    epi.load(row_base, n0, lane, w, p0);
+  }
 #pragma unroll
   for (int i = 0; i < S::TM; ++i)
 #pragma unroll
@@ -340,14 +351,7 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
         st[lr * S::kEpiLd + wn * S::WTN + j * 32 + (lane & 31)] = f32_to_bf16(acc[i][j][r]);
       }
   __syncthreads();
-  constexpr int R = Epi::kRows, G = S::kWaveRows / Epi::kRows, H = S::BN / 256;
-  static_assert(G % 2 == 0, "groups are processed in pairs");
-  const int row_base = m0 + wave * S::kWaveRows;
   if (row_base >= M) return;
-  typename Epi::Wave w;
-  epi.begin(row_base, n0, lane, min(S::kWaveRows, M - row_base), w);  // per-row loads by lane: lanes < nrows
-  typename Epi::Pre p0, p1;
-  epi.load(row_base, n0, lane, w, p0);
   const bf16_t* st_wave = st + wave * S::kWaveRows * S::kEpiLd;
 #pragma unroll 1
   for (int g = 0; g < G; g += 2) {
