@@ -427,7 +427,7 @@ struct EpiQKV {
 // h = norm(x) in bf16 (utils/model.py:46-47) with the kNDot dots h . b_k of the next linear's rank-1 terms. The tile
 // holds whole 512-wide rows (512-column tiles): lane l has columns 4l .. 4l+3 and 256 + 4l .. 256 + 4l + 3. Groups of
 // 4 rows keep the x and x0 prefetch small. The rank-1 term is added unconditionally: its a and dot are zero for rows
-// without noise.
+// without noise. x and h are written with non-temporal stores: neither is read again before it has left the caches.
 template <bool kMix, int kNDot, bool kJit = false, bool kX0 = false>
 struct EpiResidNorm {
   static constexpr int kRows = 4;
@@ -548,7 +548,7 @@ struct EpiResidNorm {
           ss[q] += xn[e] * xn[e];
         }
         v[q][hh] = xn;
-        *(f32x4*)(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane) = xn;
+        __builtin_nontemporal_store(xn, (f32x4*)(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane));
       }
     }
     const float tot = warp_sum4(ss, lane);
@@ -563,7 +563,7 @@ struct EpiResidNorm {
         const uint32_t p0 = pack_bf16x2(v[q][hh][0] * inv, v[q][hh][1] * inv);
         const uint32_t p1 = pack_bf16x2(v[q][hh][2] * inv, v[q][hh][3] * inv);
         const f32x4 hv{bf16_lo(p0), bf16_hi(p0), bf16_lo(p1), bf16_hi(p1)};
-        *(u32x2*)(h + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane) = u32x2{p0, p1};
+        __builtin_nontemporal_store((u32x2{p0, p1}), (u32x2*)(h + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane));
 #pragma unroll
         for (int k = 0; k < kNDot; ++k)
 #pragma unroll
@@ -761,6 +761,7 @@ __global__ __launch_bounds__(256) void member_sum_kernel(const float* __restrict
 
 using Tile = GemmShape<128, 256, 32, 2, 2, 3, 2>;  // two workgroups per CU: one's epilogue beside the other's MFMAs
 using RowTile = GemmShape<128, 512, 32, 2, 4>;     // whole 512-wide rows, for the epilogues that normalize
+using ProjTile = GemmShape<64, 512, 32, 1, 4, 2, 2>;  // attn_proj (K = 512): two workgroups per CU
 constexpr int kAttnOG = 1;  // 32 outputs per wave (4 waves per SIMD)
 
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -860,6 +861,8 @@ static int prepare_all() {
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<false, 1, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3, false, true>>()));
+  NOISE_CHECK_HIP((prepare_gemm<ProjTile, EpiResidNorm<false, 1>>()));
+  NOISE_CHECK_HIP((prepare_gemm<ProjTile, EpiResidNorm<false, 1, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiHeadCE>()));
   g_prepared = true;
   return NOISE_OK;
@@ -1036,9 +1039,9 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
         EpiResidNorm<false, 1, true> ej;
         memcpy((void*)&ej, (const void*)&ep, sizeof(ep));
         ej.jit = jp;
-        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ej, stream)));
+        NOISE_CHECK_HIP((launch_gemm<ProjTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ej, stream)));
       } else {
-        NOISE_CHECK_HIP((launch_gemm<RowTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
+        NOISE_CHECK_HIP((launch_gemm<ProjTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
       }
     }
 

@@ -2,9 +2,10 @@
 // the x @ weight.t() of nn.Linear weights stored [out, in]). The accumulator tile goes to an epilogue functor, which
 // is where the population-specific work (rank-1 member corrections, residual adds, relu^2, soft-capped CE) happens.
 //
-// Tiling: a workgroup computes 256 x 256 with 2 x 2 waves, or 128 x 512 with 1 x 4 waves (whole 512-wide rows, for
-// epilogues that normalize rows); a wave owns 128 x 128 as 4 x 4 MFMA tiles (v_mfma_f32_32x32x16_bf16). The
-// 128 x 256 tile (waves of 64 x 128) is sized for two workgroups per CU, so that one workgroup's epilogue runs beside
+// Tiling: a workgroup computes 256 x 256 with 2 x 2 waves of 128 x 128 (4 x 4 MFMA tiles of
+// v_mfma_f32_32x32x16_bf16), or one of the tiles with waves of 64 x 128: 128 x 512 with 2 x 4 waves and 64 x 512
+// with 1 x 4 waves (whole 512-wide rows, for epilogues that normalize rows), 128 x 256 with 2 x 2 waves. The
+// 128 x 256 and 64 x 512 tiles are sized for two workgroups per CU, so that one workgroup's epilogue runs beside
 // the other's MFMAs. K advances in steps of 32 through kStages LDS stages filled by direct-to-LDS buffer loads
 // (buffer_load_dwordx4 ... lds): the loads of step kt + kStages are issued as soon as every wave is done with step
 // kt, so kStages - 1 steps of loads are in flight behind the MFMAs and no register holds staged data.
