@@ -311,8 +311,10 @@ __global__ __launch_bounds__(256) void gate_kernel(Members mb, const bf16_t* __r
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; }
 
+// Streaming store of 4 bf16: the GEMM outputs are read next by another kernel, after they have left the caches, so
+// the stores are non-temporal.
 __device__ __forceinline__ void st_bf16x4(bf16_t* p, f32x4 v) {
-  *(u32x2*)p = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  __builtin_nontemporal_store((u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}), (u32x2*)p);
 }
 
 // q|k|v = h W_qkv^T + s (h . b_seg) a_seg (eggroll.py:80-84); on q and k columns then the rotary embedding and the
@@ -640,7 +642,7 @@ struct EpiReluSqT {
         v[q][e] = r * r;
       }
       pk[q] = u32x2{pack_bf16x2(v[q][0], v[q][1]), pack_bf16x2(v[q][2], v[q][3])};
-      *(u32x2*)(out + (int64_t)(row0 + q) * ldo + n0 + 4 * lane) = pk[q];
+      __builtin_nontemporal_store(pk[q], (u32x2*)(out + (int64_t)(row0 + q) * ldo + n0 + 4 * lane));
     }
     if (w.nr) {
       static_assert(R == 8, "warp_sum8 reduces 8 rows");
