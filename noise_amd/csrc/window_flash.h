@@ -450,6 +450,9 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, OPT>)) void window_flas
       if (MODE == kAttn) {
         const float inv = 1.0f / l_tot;
         bf16_t* og_ptr = (bf16_t*)a.out + b * a.o_sb + (int64_t)my_o * a.o_st + head * 64;
+        // One wave's 32 x 64 output tile in the input-tile LDS, free after the loop's last barrier: 4 waves x 4 KB
+        static_assert(4 * 32 * 64 <= 2 * 64 * 64, "4 waves' staged tiles fit the input-tile LDS");
+        bf16_t* y_stage = &ys[0][0] + wave * 2048;
         float dot = 0.f;
         const float* bv = a.xb_out ? a.xb_vec + (int64_t)a.xb_row[b] * a.xb_stride + head * 64 : nullptr;
         const bool jit = a.jit_sigma != 0.f;
@@ -474,8 +477,27 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, OPT>)) void window_flas
                                  o_acc[og][dt][g * 4 + 2 * j + 1] * inv + jz[2 * j + 1]);
               if (bv) dot += bf16_lo(e[j]) * bv[d + 2 * j] + bf16_hi(e[j]) * bv[d + 2 * j + 1];
             }
-            *(u32x2*)(og_ptr + d) = u32x2{e[0], e[1]};
+            if constexpr (OG == 1) {  // staged: row col of the wave's 32 x 64 tile, 16-byte unit swizzled by row
+              const int u = (dt * 4 + g) ^ ((col >> 1) & 7);
+              *(u32x2*)(y_stage + col * 64 + u * 8 + half * 4) = u32x2{e[0], e[1]};
+            } else {
+              *(u32x2*)(og_ptr + d) = u32x2{e[0], e[1]};
+            }
           }
+        if constexpr (OG == 1) {
+          // The staged tile leaves as whole 128-byte rows: 8 rows per store instruction, non-temporal (attn_proj
+          // reads y after it has left the caches). Only this wave's lanes touch its staging slice.
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int r = k * 8 + (lane >> 3), u = lane & 7;
+            const u32x4 val = *(const u32x4*)(y_stage + r * 64 + ((u ^ ((r >> 1) & 7)) * 8));
+            __builtin_nontemporal_store(
+                val, (u32x4*)((bf16_t*)a.out + b * a.o_sb + (int64_t)(ow + r) * a.o_st + head * 64 + u * 8));
+          }
+        }
         if (a.xb_out) {
           dot += lane_xor32(dot, lane);
           if (half == 0) a.xb_out[(b * T + my_o) * a.heads + head] = dot;
