@@ -277,15 +277,25 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
 
 // gate[r, hd] = 2 sigmoid(h[r, :32] . W_g[hd] + s (h[r, :32] . b_g) a_g[hd]) (eggroll.py:85-89), for a block with
 // value embeddings whose h comes from a GEMM epilogue; 8 lanes per row, lane hd of the row computes head hd. The
-// channel sums go in chunks of 8 combined pairwise, as in mix_norm_kernel.
+// channel sums go in chunks of 8 combined pairwise, as in mix_norm_kernel. A workgroup's 32 rows belong to one member
+// (T % 128 == 0), so W_g and the member's a_g, b_g are staged in LDS once per workgroup.
 __global__ __launch_bounds__(256) void gate_kernel(Members mb, const bf16_t* __restrict__ h,
                                                    const float* __restrict__ w_gate, int64_t off_gate,
                                                    float* __restrict__ gate, int64_t M) {
-  const int64_t r = blockIdx.x * 32 + (threadIdx.x >> 3);
+  static_assert(kH * kGateIn == 256, "one W_g element per thread");
+  __shared__ __align__(16) float wg[kH * kGateIn];
+  __shared__ __align__(16) float bg[kGateIn];
+  __shared__ float ag[kH];
+  const int64_t r0 = (int64_t)blockIdx.x * 32;  // < M: the grid has ceil(M / 32) workgroups
+  const int m = mb.member(r0);
+  const float* nr = mb.nrow(m);
+  wg[threadIdx.x] = w_gate[threadIdx.x];
+  if (nr && threadIdx.x < kGateIn) bg[threadIdx.x] = nr[off_gate + kH + threadIdx.x];
+  if (nr && threadIdx.x < kH) ag[threadIdx.x] = nr[off_gate + threadIdx.x];
+  __syncthreads();
+  const int64_t r = r0 + (threadIdx.x >> 3);
   if (r >= M) return;
   const int hd = threadIdx.x & 7;
-  const int m = mb.member(r);
-  const float* nr = mb.nrow(m);
   const float s = mb.sgn(m);
   float g[4], db[4];
 #pragma unroll
@@ -294,15 +304,20 @@ __global__ __launch_bounds__(256) void gate_kernel(Members mb, const bf16_t* __r
     float hv[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) { hv[2 * j] = __uint_as_float(p[j] << 16); hv[2 * j + 1] = __uint_as_float(p[j] & 0xFFFF0000u); }
+    const f32x4 w0 = *(const f32x4*)&wg[hd * kGateIn + 8 * c], w1 = *(const f32x4*)&wg[hd * kGateIn + 8 * c + 4];
+    const float w[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
     g[c] = 0.f; db[c] = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      g[c] += hv[j] * w_gate[hd * kGateIn + 8 * c + j];
-      if (nr) db[c] += hv[j] * nr[off_gate + kH + 8 * c + j];
+    for (int j = 0; j < 8; ++j) g[c] += hv[j] * w[j];
+    if (nr) {
+      const f32x4 b0 = *(const f32x4*)&bg[8 * c], b1 = *(const f32x4*)&bg[8 * c + 4];
+      const float bb[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) db[c] += hv[j] * bb[j];
     }
   }
   float pre = (g[0] + g[1]) + (g[2] + g[3]);
-  if (nr) pre += s * ((db[0] + db[1]) + (db[2] + db[3])) * nr[off_gate + hd];
+  if (nr) pre += s * ((db[0] + db[1]) + (db[2] + db[3])) * ag[hd];
   gate[r * kH + hd] = 2.0f / (1.0f + expf(-pre));
 }
 
