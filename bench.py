@@ -44,12 +44,12 @@ def zipf_tokens(n_rows, T, seed, vocab=V, s=1.1):
     return rows[:, :-1].contiguous(), rows[:, 1:].contiguous()
 
 
-def make_model(dev, seed=0):
+def make_model(dev, seed=0, n_layer=8):
     import torch
     from noise_amd.model import GPT, GPTConfig
     torch.manual_seed(seed)
     with torch.device('meta'):
-        model = GPT(GPTConfig())
+        model = GPT(GPTConfig(n_layer=n_layer))
     model.to_empty(device=dev)
     model.init_weights()
     model.transformer.wte.float()
@@ -122,11 +122,11 @@ def roofline_from_timing(timing, flops, traffic=None):
     return roof, kernels
 
 
-def bench_c4(args, dev):
+def bench_c4(args, dev, n_layer=8):
     import torch
     from noise_amd import _lib
     from noise_amd.population import Eggroll, NoiseLayout, run_forward
-    model = make_model(dev)
+    model = make_model(dev, n_layer=n_layer)
     pairs, n_seq = 128, 2
     members = 2 * pairs
     x, y = zipf_tokens(n_seq, T_SEQ, seed=0)
@@ -145,7 +145,7 @@ def bench_c4(args, dev):
         table = es.offset_table(i)
         rows = es.rows(table, all_dirs)
         out = run_forward(model, x, y, member_seq, noise=rows, member_row=member_row, member_sign=member_sign,
-                          layout=layout)
+                          layout=layout, check_tables=False)
         return out['loss_sum'].view(members, n_seq).sum(1)
 
     for i in range(args.warmup):
@@ -164,11 +164,15 @@ def bench_c4(args, dev):
     windows = [w for w, _ in model.window_sizes]
     roof, kernels = roofline_from_timing(timing, kernel_flops(members * n_seq, T_SEQ, windows, len(windows)),
                                          load_traffic())
+    flops = kernel_flops(members * n_seq, T_SEQ, windows, len(windows))
+    step_flop = len(windows) * sum(flops[k] for k in ('qkv_gemm', 'attn_proj_gemm', 'fc_gemm', 'mlp_proj_gemm',
+                                                      'attention')) + flops['head_ce_gemm']
     res = dict(value=member_tokens * args.steps / dt, ms_per_step=dt / args.steps * 1e3, member_tokens=member_tokens,
-               roofline=roof, kernels=kernels, finite=finite,
+               roofline=roof, kernels=kernels, finite=finite, step_flop=step_flop,
                mean_member_ce=float(losses.mean().item() / (n_seq * T_SEQ)),
-               config=dict(workload='C4: 8-layer population forward, 256 antithetic members (128 pairs) x 2 '
-                           'sequences x 2048 Zipf(1.1) tokens, vocab 4096, N(0,0.02) weights, in-kernel counter noise',
+               config=dict(workload=f'C4: {len(windows)}-layer population forward, 256 antithetic members (128 '
+                           'pairs) x 2 sequences x 2048 Zipf(1.1) tokens, vocab 4096, N(0,0.02) weights, in-kernel '
+                           'counter noise',
                            members=members, sequences_per_member=n_seq, seq_len=T_SEQ, n_layer=len(windows),
                            params=sum(p.numel() for p in model.parameters()), parallelism='single GPU'))
     res['model'] = model
@@ -194,8 +198,8 @@ def bench_c5(args, dev, steps=None, warmup=None):
     ck = (torch.randn(n_seq * 8, T_SEQ, 64, device=dev, generator=g) / 8).bfloat16()
     ce = torch.randn(n_seq * 8, T_SEQ, 64, device=dev, generator=g)
     n_layer = model.config.n_layer
-    if (cq.float().norm(dim=-1).max() * ck.float().norm(dim=-1).max()).item() / 8 > 80:
-        raise RuntimeError('c5 bench: the credit logits exceed the bounded LSE pass\'s 80')
+    if (cq.float().norm(dim=-1).max() * ck.float().norm(dim=-1).max()).item() / 8 > 16:
+        raise RuntimeError('c5 bench: the credit logits exceed the bounded LSE pass\'s 16')
 
     def step(i):
         loss = es.step(x, y, opt, i)
@@ -248,6 +252,23 @@ def bench_c5(args, dev, steps=None, warmup=None):
     return res
 
 
+def c4_12layer_record(dev, steps=5, warmup=1):
+    """BASELINE.json's configs[3] read literally: the config-4 population forward on the 12-layer model (GPTConfig
+    n_layer=12, 54.5M parameters; windows SSSL repeated, value embeddings on alternate layers), same members, tokens
+    and noise as the headline, fewer steps."""
+    import types
+    res = bench_c4(types.SimpleNamespace(steps=steps, warmup=warmup), dev, n_layer=12)
+    res.pop('model')
+    tf = res['step_flop'] / (res['ms_per_step'] * 1e-3) / 1e12
+    return dict(workload=res['config']['workload'], n_layer=12, params=res['config']['params'], steps=steps,
+                warmup=warmup, ms_per_step=round(res['ms_per_step'], 3),
+                member_tokens_per_s=round(res['value'], 1),
+                flop_per_member_token=round(res['step_flop'] / res['member_tokens'], 1),
+                forward_tflops=round(tf, 1), forward_frac=round(tf / PEAK_BF16_TFLOPS, 4), finite=res['finite'],
+                kernels={k: dict(avg_ms=v['avg_ms'], tflops=v.get('tflops')) for k, v in res['kernels'].items()
+                         if 'tflops' in v})
+
+
 def c5_record(dev):
     """Config 5 in the default run: 1 warmup step, then 2 timed steps, each a full EGGROLL update."""
     import types
@@ -264,7 +285,7 @@ def c5_record(dev):
 def bench_credit(dev, iters=10):
     """Config 3: lse + value pass, B16 H8 T2048 d64, Q/K bf16 N(0,1)/8, E N(0,1) fp32, full causal window and 1024;
     also the key-context pass (lse and center) on the same q / k with bf16 values and hub. The LSE pass runs its
-    bounded form (no running maximum), after a check that max|q| max|k| / 8, a bound on every logit, is <= 80."""
+    bounded form (no running maximum), after a check that max|q| max|k| / 8, a bound on every logit, is <= 16."""
     import torch
     from noise_amd import _lib, credit
     rows, T = 16 * 8, 2048
@@ -274,8 +295,8 @@ def bench_credit(dev, iters=10):
     e = torch.randn(rows, T, 64, device=dev, generator=g)
     pairs = rows * T * (T + 1) // 2
     logit_bound = (q.float().norm(dim=-1).max() * k.float().norm(dim=-1).max()).item() / 8  # Cauchy-Schwarz
-    if logit_bound > 80:
-        raise RuntimeError(f'credit bench: logits up to {logit_bound:.1f} exceed the bounded LSE pass\'s 80')
+    if logit_bound > 16:
+        raise RuntimeError(f'credit bench: logits up to {logit_bound:.1f} exceed the bounded LSE pass\'s 16')
     out = {'logit_bound': round(logit_bound, 3)}
     for window in (T, 1024):
         npairs = rows * sum(min(t, window) + 1 for t in range(T))
@@ -582,6 +603,60 @@ def cpu_baseline(model, sample_members=4, T=T_SEQ, reps=3):
     return out
 
 
+def peak_calibration(dev, iters=40000, workgroups=2048, reps=3, copy_bytes=4 << 30):
+    """Measured ceilings on this box: the sustained bf16 MFMA rate (noise_peak_mfma: every CU, 8 independent
+    v_mfma_f32_32x32x16_bf16 chains per wave, 2 waves per SIMD) on random N(0, 1) operands held in registers, on the
+    same operands streamed from LDS every step (a GEMM main loop's fragment reads), and on zero operands (the clock
+    depends on the operand bits); and the HBM rate of a plain device-to-device copy of 4 GiB (read + write bytes).
+    Each figure is the best of `reps` launches timed with HIP events on the launch stream."""
+    import torch
+    from noise_amd import _lib
+    n_rows = 4096
+    g = torch.Generator(device=dev).manual_seed(17)
+    rand = torch.randn(n_rows * 64 * 8, device=dev, generator=g).bfloat16()
+    zero = torch.zeros_like(rand)
+    out = torch.empty(workgroups * 256, device=dev)
+    flop = workgroups * 4 * iters * 8 * 32768.0
+    res = dict(unit='TFLOP/s', iters=iters, workgroups=workgroups, flop_per_launch=flop)
+    stream = torch.cuda.current_stream(dev)
+    for name, ops, lds in (('mfma_random_registers', rand, 0), ('mfma_random_lds', rand, 1),
+                           ('mfma_zero_registers', zero, 0)):
+        best = 0.0
+        _lib.call('noise_peak_mfma', _lib.ptr(ops), n_rows, iters // 8, workgroups, lds, _lib.ptr(out),
+                  _lib.stream(dev))  # warm-up (a shorter launch)
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            _lib.call('noise_peak_mfma', _lib.ptr(ops), n_rows, iters, workgroups, lds, _lib.ptr(out),
+                      _lib.stream(dev))
+            e1.record(stream)
+            torch.cuda.synchronize()
+            best = max(best, flop / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+        if not torch.isfinite(out).all():
+            raise RuntimeError('peak calibration: non-finite accumulators')
+        res[name] = round(best, 1)
+        # the engine clock the rate implies, against the 2.5 PFLOP/s at 2.4 GHz of the spec sheet
+        res[name + '_ghz'] = round(best / PEAK_BF16_TFLOPS * 2.4, 3)
+    a = torch.ones(copy_bytes // 4, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    best = 0.0
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        b.copy_(a)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = max(best, 2.0 * copy_bytes / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    res['hbm_copy_gbs'] = round(best, 1)
+    res['hbm_copy_bytes'] = copy_bytes
+    del a, b
+    res['note'] = ('mfma_*: TFLOP/s of a sustained v_mfma_f32_32x32x16_bf16 stream over every CU; _ghz: the clock '
+                   'that rate implies (2.5 PFLOP/s at 2.4 GHz). hbm_copy_gbs: read + write bytes of one 4 GiB '
+                   'device copy per second. The roofline\'s measured_peak is mfma_random_registers.')
+    return res
+
+
 def copy_calibration(dev, nbytes=1 << 30):
     """One device-to-device copy of `nbytes`: reads and writes exactly nbytes of HBM."""
     import torch
@@ -606,6 +681,8 @@ def main():
     ap.add_argument('--no-dust', action='store_true', help="skip the head-slab estimator's line")
     ap.add_argument('--copy-calibration', action='store_true',
                     help='run one plain device copy of exactly 1 GiB and exit (rocprofv3 counter calibration)')
+    ap.add_argument('--peak-calibration', action='store_true',
+                    help='measure the sustained MFMA rate and the device-copy HBM rate on this box, print them, exit')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         sys.exit('bench.py measures one GPU: this build runs the hot path on a single MI355X; '
@@ -618,6 +695,10 @@ def main():
     if args.copy_calibration:
         copy_calibration(dev)
         return
+    if args.peak_calibration:
+        print(json.dumps(dict(peak_calibration=peak_calibration(dev))), flush=True)
+        return
+    calib = peak_calibration(dev)
     res = bench_c4(args, dev) if args.workload == 'c4' else bench_c5(args, dev)
     model = res.pop('model')
     line = dict(metric=METRIC, value=round(res['value'], 1), unit='member-tokens/s', n_gpus=1, steps=args.steps,
@@ -626,6 +707,11 @@ def main():
                 config=res['config'], roofline=res['roofline'])
     line['roofline']['forward_tflops'] = round(res['value'] * FLOP_PER_MEMBER_TOKEN / 1e12, 1)
     line['roofline']['forward_frac'] = round(res['value'] * FLOP_PER_MEMBER_TOKEN / 1e12 / PEAK_BF16_TFLOPS, 4)
+    measured = calib['mfma_random_registers']
+    line['roofline']['measured_peak'] = measured
+    line['roofline']['frac_of_measured'] = round(line['roofline']['achieved'] / measured, 4)
+    line['roofline']['forward_frac_of_measured'] = round(line['roofline']['forward_tflops'] / measured, 4)
+    line['peak_calibration'] = calib
     line['kernels'] = res['kernels']
     line['finite'] = res['finite']
     if 'update' in res:
@@ -636,6 +722,8 @@ def main():
         line['c2'] = bench_c2(dev)
     if not args.no_c5 and args.workload == 'c4':
         line['c5'] = c5_record(dev)
+    if args.workload == 'c4':
+        line['c4_12layer'] = c4_12layer_record(dev)
     if not args.no_dust:
         line['dust_head_error'] = bench_head_error(dev)
         line['dust_direct'] = bench_dust_direct(dev, model)

@@ -34,6 +34,15 @@ int noise_abi_version(void);
 int noise_timing_enable(int enable);
 int noise_timing_read(int32_t n, int64_t* counts, double* total_ms, const char** names);
 
+/* Measured ceiling for the roofline (no counterpart in the reference, which publishes no kernel rates): a sustained
+ * stream of v_mfma_f32_32x32x16_bf16 over `workgroups` workgroups of 4 waves, each wave `iters` steps of 8 MFMAs
+ * (32,768 FLOP each) on 8 independent accumulators. ops bf16 [n_frag_rows, 64 lanes, 8] (n_frag_rows >= 32) supplies
+ * the operand bits (the engine clock under load depends on them); lds = 0 holds each wave's 6 fragments in registers,
+ * lds = 1 reads every step's 6 fragments from a 32 KB LDS block (iters even), as a GEMM main loop does. out fp32
+ * [workgroups * 256]. FLOPs = workgroups * 4 * iters * 8 * 32768. */
+int noise_peak_mfma(const uint16_t* ops, int64_t n_frag_rows, int32_t iters, int32_t workgroups, int32_t lds,
+                    float* out, void* stream);
+
 /* ---- a1: counter-based noise (replaces the 2^28-value torch.randn buffer and the torch.randint offsets) -------- */
 
 /* out[j] = G[start + j], the virtual N(0,1) buffer of Philox4x32-10 + Box-Muller values.
@@ -141,6 +150,7 @@ typedef struct noise_gpt {
 typedef struct noise_perturbation {
   const float* rows;          /* fp32 [n_rows, stride] */
   int64_t stride;
+  int64_t n_rows;             /* rows of `rows` (>= 1 when rows != NULL): the range member_row is checked against */
   int64_t resid_lambdas, x0_lambdas, wte, lm_head;
   int64_t c_q[NOISE_MAX_LAYERS], c_k[NOISE_MAX_LAYERS], c_v[NOISE_MAX_LAYERS], c_proj[NOISE_MAX_LAYERS];
   int64_t ve_gate[NOISE_MAX_LAYERS], c_fc[NOISE_MAX_LAYERS], mlp_proj[NOISE_MAX_LAYERS], ve[NOISE_MAX_LAYERS];
@@ -148,6 +158,8 @@ typedef struct noise_perturbation {
 
 /* Evaluates `members` perturbed models, member i on token row member_seq[i] with noise row member_row[i] scaled by
  * member_sign[i] (+-sigma), T tokens each (T % 128 == 0). tokens / targets int64 [n_seq, T]; a target < 0 is ignored.
+ * The member tables live on the device and are checked there: a member whose member_seq is outside [0, n_seq) or
+ * whose member_row is outside [0, pert->n_rows) reads nothing out of range and gets a NaN loss (every token NaN).
  * Outputs (each may be NULL): loss_sum fp32 [members] = summed next-token CE of each member; token_loss fp32
  * [members, T]; logits fp32 [members, T, vocab] (soft-capped, 15 tanh(z / 15)).
  * workspace: noise_population_forward_workspace(members, T) bytes of device memory.
@@ -218,10 +230,12 @@ int noise_adamw_batch(int32_t n, float* const* p, const float* const* g, float* 
  * Replaces: train/speedrun/moment_kernels.py:79-110, 137-164 (_implicit_key_statistics, its lse output). */
 int noise_credit_lse(const uint16_t* q, const uint16_t* k, int64_t rows, int64_t T, int32_t window, float* lse,
                      void* stream);
-/* noise_credit_lse for callers whose logits are bounded, |q . k| / 8 <= 80 on every in-window pair (q and k
+/* noise_credit_lse for callers whose logits are bounded, |q . k| / 8 <= 16 on every in-window pair (q and k
  * RMS-normalized over their 64 channels give <= 8, as the model's do): the sum of exp(logit) then stays inside fp32
- * with no running maximum, and each logit costs one exp2 (q carries the scale log2(e) / 8, one more bf16 rounding).
- * Larger logits overflow the sum (lse inf or NaN). Same arguments and errors as noise_credit_lse.
+ * with no running maximum at any T and window (e^16 times 2^31 terms is below 2^128), and each logit costs one exp2
+ * (q carries the scale log2(e) / 8: one more bf16 rounding of q, which moves a logit by at most 16 * 2^-9 = 0.03 at
+ * the bound). Larger logits lose accuracy and, near 88, overflow the sum (lse inf or NaN). Same arguments and errors
+ * as noise_credit_lse.
  * Replaces: train/speedrun/moment_kernels.py:79-110 (_implicit_key_statistics' lse) where its inputs are bounded. */
 int noise_credit_lse_bounded(const uint16_t* q, const uint16_t* k, int64_t rows, int64_t T, int32_t window,
                              float* lse, void* stream);

@@ -11,7 +11,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load order: torch's HIP runtime first)
 
 LIB_PATH = Path(__file__).resolve().parent / 'libnoise_amd.so'
-ABI_VERSION = 3  # include/noise_amd.h's signatures (noise_abi_version)
+ABI_VERSION = 4  # include/noise_amd.h's signatures (noise_abi_version)
 MAX_LAYERS = 16
 
 c_p = ctypes.c_void_p
@@ -30,7 +30,7 @@ class NoiseGpt(ctypes.Structure):
 
 
 class NoisePerturbation(ctypes.Structure):
-    _fields_ = [('rows', c_p), ('stride', i64), ('resid_lambdas', i64), ('x0_lambdas', i64), ('wte', i64),
+    _fields_ = [('rows', c_p), ('stride', i64), ('n_rows', i64), ('resid_lambdas', i64), ('x0_lambdas', i64), ('wte', i64),
                 ('lm_head', i64)] + [(n, i64 * MAX_LAYERS) for n in
                                      ('c_q', 'c_k', 'c_v', 'c_proj', 've_gate', 'c_fc', 'mlp_proj', 've')]
 
@@ -45,6 +45,7 @@ _SIGNATURES = {
     'noise_abi_version': ([], ctypes.c_int),
     'noise_timing_enable': ([ctypes.c_int], ctypes.c_int),
     'noise_timing_read': ([i32, c_p, c_p, c_p], ctypes.c_int),
+    'noise_peak_mfma': ([c_p, i64, i32, i32, i32, c_p, c_p], ctypes.c_int),
     'noise_rng_buffer': ([u64, u64, i64, c_p, c_p], ctypes.c_int),
     'noise_rng_offsets': ([u64, u64, c_p, i32, i64, c_p, c_p], ctypes.c_int),
     'noise_rng_rows': ([u64, c_p, i64, c_p, i32, c_p, i64, c_p, c_p], ctypes.c_int),

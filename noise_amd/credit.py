@@ -45,8 +45,9 @@ def _match(q, **others):
 
 def credit_lse(q: torch.Tensor, k: torch.Tensor, window: int, bounded: bool = False) -> torch.Tensor:
     """lse [rows, T] of each query's window logits q_s . k_t / 8 (q, k: (rows, T, 64), cast to bf16). bounded: the
-    caller guarantees |q_s . k_t| / 8 <= 80 on every in-window pair (RMS-normed q and k give <= 8); the pass then keeps
-    no running maximum (noise_credit_lse_bounded)."""
+    caller guarantees |q_s . k_t| / 8 <= 16 on every in-window pair (RMS-normed q and k give <= 8); the pass then keeps
+    no running maximum (noise_credit_lse_bounded): the sum of exp(logit) cannot overflow fp32 at any window, and the
+    one extra bf16 rounding of q (it carries the scale) moves a logit by at most 16 * 2^-9 = 0.03."""
     rows, T = _match(q, k=k)
     _lib.require_device(q, k)
     q = q.to(torch.bfloat16).contiguous()

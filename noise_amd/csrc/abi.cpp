@@ -19,7 +19,7 @@ int noise_set_error(int code, const char* fmt, ...) {
 
 extern "C" const char* noise_last_error(void) { return g_error; }
 
-extern "C" int noise_abi_version(void) { return 3; }
+extern "C" int noise_abi_version(void) { return 4; }
 
 // ---- timing -----------------------------------------------------------------------------------------------------
 namespace {

@@ -18,8 +18,9 @@ namespace noise {
 
 constexpr int kDcMaxT = 8192;  // positions per row held in LDS
 
-__global__ __launch_bounds__(256) void decayed_credit_kernel(const float* __restrict__ score, int T, int inner,
-                                                             int W, float gamma, float* __restrict__ out) {
+// score and out carry no __restrict__: out may be score itself (dust.decayed_credit calls it in place).
+__global__ __launch_bounds__(256) void decayed_credit_kernel(const float* score, int T, int inner, int W, float gamma,
+                                                             float* out) {
   __shared__ float e_s[kDcMaxT];
   __shared__ float suffix[256];
   __shared__ float wave_total[4];

@@ -15,6 +15,9 @@ namespace noise {
 
 constexpr float kNormEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps, F.rms_norm's default
 
+// The member tables. A member whose token row is outside [0, n_seq) or whose noise row is outside [0, n_rows) reads
+// row 0 of both (so every access stays inside its buffer) and is marked bad: the embedding gives its rows NaN and the
+// CE finalization writes NaN for every one of its tokens, so its loss is NaN (the reference's indexing would raise).
 struct Members {
   int T;
   const int32_t* seq;   // token row of each member
@@ -23,12 +26,19 @@ struct Members {
   const float* noise;   // [n_rows, stride] or NULL (unperturbed)
   int64_t stride;
   const int64_t* tokens;   // [n_seq, T]
+  int64_t n_seq, n_rows;
   __device__ __forceinline__ int member(int64_t r) const { return (int)(r / T); }
-  __device__ __forceinline__ const float* nrow(int m) const { return noise ? noise + (int64_t)row[m] * stride : nullptr; }
+  __device__ __forceinline__ bool seq_ok(int m) const { return (uint32_t)seq[m] < (uint64_t)n_seq; }
+  __device__ __forceinline__ bool row_ok(int m) const { return !noise || (uint32_t)row[m] < (uint64_t)n_rows; }
+  __device__ __forceinline__ bool bad(int m) const { return !(seq_ok(m) && row_ok(m)); }
+  __device__ __forceinline__ int sq(int m) const { return seq_ok(m) ? seq[m] : 0; }  // the member's token row
+  __device__ __forceinline__ const float* nrow(int m) const {
+    return noise ? noise + (int64_t)(row_ok(m) ? row[m] : 0) * stride : nullptr;
+  }
   __device__ __forceinline__ float sgn(int m) const { return noise ? sign[m] : 0.f; }
   __device__ __forceinline__ int64_t token(int64_t r) const {
     const int m = member(r);
-    return tokens[(int64_t)seq[m] * T + (r - (int64_t)m * T)];
+    return tokens[(int64_t)sq(m) * T + (r - (int64_t)m * T)];
   }
 };
 
@@ -44,7 +54,7 @@ struct Jitter {
   // sigma a at member row r, channels c .. c + 3 of a site `width` wide
   __device__ __forceinline__ f32x4 quad(const Members& mb, int64_t r, int width, int c) const {
     const int m = mb.member(r);
-    const uint32_t row = (uint32_t)((int64_t)mb.seq[m] * mb.T + (r - (int64_t)m * mb.T));
+    const uint32_t row = (uint32_t)((int64_t)mb.sq(m) * mb.T + (r - (int64_t)m * mb.T));
     float z[4];
     dust_noise_quad(seed, (uint32_t)(draw0 + m / n_seq), site, row, (uint32_t)(width / 4), (uint32_t)(c / 4), z);
     return f32x4{sigma * z[0], sigma * z[1], sigma * z[2], sigma * z[3]};
@@ -82,7 +92,7 @@ __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __r
   float at = 0.f;
   if (lane < 8) {
     const int64_t t = mb.token(r0 + lane);
-    bad = t < 0 || t >= Vp;
+    bad = t < 0 || t >= Vp || mb.bad(m);
     tk = bad ? 0 : (int)t;
     if (nr) at = s * nr[off_wte + tk];
   }
@@ -374,7 +384,7 @@ struct EpiQKV {
       if (lane < nrows) w.xb = xb[(int64_t)(row_base + lane) * 4 + w.seg];
     }
     if (w.seg == 2 && ve) {
-      const int64_t tk = lane < nrows ? mb.tokens[(int64_t)mb.seq[m] * mb.T + w.t0 + lane] : 0;
+      const int64_t tk = lane < nrows ? mb.tokens[(int64_t)mb.sq(m) * mb.T + w.t0 + lane] : 0;
       w.tok = (tk < 0 || tk >= Vp) ? 0 : (int)tk;
       if (w.nr) {
         w.at = w.nr[off_ve + w.tok];  // times the sign in ready()
@@ -719,7 +729,7 @@ struct EpiHeadCE {
   __device__ __forceinline__ void begin(int row_base, int n0, int lane, int nrows, Wave& w) const {
     const int m = mb.member(row_base);
     w.row_base = row_base;
-    w.t = lane < nrows ? targets[(int64_t)mb.seq[m] * mb.T + (row_base - m * mb.T) + lane] : -1;
+    w.t = lane < nrows ? targets[(int64_t)mb.sq(m) * mb.T + (row_base - m * mb.T) + lane] : -1;
     w.tg = -1;
     w.nr = mb.nrow(m);
     w.s = 0.f; w.xb = 0.f;
@@ -788,7 +798,8 @@ struct EpiHeadCE {
   }
 };
 
-// per-row CE from the column-tile sums: lse = 15 + log(sum); a negative target contributes 0, an out-of-range one NaN.
+// per-row CE from the column-tile sums: lse = 15 + log(sum); a negative target contributes 0, an out-of-range one NaN,
+// and every token of a member with an out-of-range table entry NaN.
 __global__ void ce_finalize_kernel(Members mb, const float* __restrict__ part_sum, int n_part,
                                    const float* __restrict__ tgt_logit, const int64_t* __restrict__ targets, int vocab,
                                    float* __restrict__ row_ce, float* __restrict__ token_loss, int64_t M) {
@@ -797,9 +808,10 @@ __global__ void ce_finalize_kernel(Members mb, const float* __restrict__ part_su
   float sum = 0.f;
   for (int p = 0; p < n_part; ++p) sum += part_sum[r * n_part + p];
   const int m = mb.member(r);
-  const int64_t tg = targets[(int64_t)mb.seq[m] * mb.T + (r - (int64_t)m * mb.T)];
+  const int64_t tg = targets[(int64_t)mb.sq(m) * mb.T + (r - (int64_t)m * mb.T)];
   float ce;
-  if (tg < 0) ce = 0.f;
+  if (mb.bad(m)) ce = __builtin_nanf("");
+  else if (tg < 0) ce = 0.f;
   else if (tg >= vocab) ce = __builtin_nanf("");
   else ce = 15.0f + logf(sum) - tgt_logit[r];
   row_ce[r] = ce;
@@ -897,7 +909,7 @@ __global__ __launch_bounds__(256) void replicate_rows_kernel(Members mb, const f
   const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= M) return;
   const int lane = threadIdx.x & 63, m = mb.member(r);
-  const float* s = src + ((int64_t)mb.seq[m] * mb.T + (r - (int64_t)m * mb.T)) * kD + lane * 8;
+  const float* s = src + ((int64_t)mb.sq(m) * mb.T + (r - (int64_t)m * mb.T)) * kD + lane * 8;
   float* d = dst + r * kD + lane * 8;
   *(f32x4*)d = *(const f32x4*)s;
   *(f32x4*)(d + 4) = *(const f32x4*)(s + 4);
@@ -990,7 +1002,11 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
   int rc = prepare_all();
   if (rc) return rc;
 
-  Members mb{(int)T, member_seq, member_row, member_sign, pert->rows, pert->stride, tokens};
+  NOISE_REQUIRE(!pert->rows || (pert->n_rows > 0 && pert->n_rows <= INT32_MAX && pert->stride > 0),
+                "perturbation rows given: n_rows = %lld must be in [1, 2^31) and the stride positive",
+                (long long)pert->n_rows);
+  // member tables are read on the device: an entry outside [0, n_seq) or [0, n_rows) makes that member's loss NaN
+  Members mb{(int)T, member_seq, member_row, member_sign, pert->rows, pert->stride, tokens, n_seq, pert->n_rows};
   const int Vp = model->padded_vocab;
   const bool noisy = pert->rows != nullptr;
   const unsigned row_blocks = (unsigned)((M + 3) / 4);
@@ -1071,7 +1087,7 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
     fa.out = ws.y; fa.o_sb = T * kD; fa.o_st = kD;
     fa.xb_out = noisy ? ws.xbp : nullptr;
     fa.xb_vec = noisy ? pert->rows + pert->c_proj[i] + kD : nullptr;
-    fa.xb_row = member_row; fa.xb_stride = pert->stride;
+    fa.xb_row = member_row; fa.xb_stride = pert->stride; fa.xb_rows = pert->n_rows;
     fa.heads = kH; fa.T = (int)T; fa.window = L.window;
     {
       const Jitter jo = dr->jit(i, 1);

@@ -82,7 +82,7 @@ extern "C" int noise_credit_lse_bounded(const uint16_t* q, const uint16_t* k, in
   a.lse_out = lse;
   a.heads = 1; a.T = (int)T; a.window = window;
   NoiseTimer tm(kTimeCreditLse, (hipStream_t)stream);
-  NOISE_CHECK_HIP((launch_flash<kLse, true, 1>(a, rows, 1, (hipStream_t)stream)));  // the caller's |q . k| / 8 <= 80
+  NOISE_CHECK_HIP((launch_flash<kLse, true, 1>(a, rows, 1, (hipStream_t)stream)));  // the caller's |q . k| / 8 <= 16
   return NOISE_OK;
 }
 

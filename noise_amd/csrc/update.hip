@@ -444,11 +444,13 @@ extern "C" int noise_adamw_batch(int32_t n, float* const* p, const float* const*
   }
   const AdamScalars s = adam_scalars(lr, beta1, beta2, eps, weight_decay, step);
   NoiseTimer tm(kTimeAdamw, (hipStream_t)stream);
-  for (int32_t j0 = 0; j0 < n; j0 += kAdamMaxJobs) {
+  // One cursor over the tensors: each launch takes the next kAdamMaxJobs non-empty ones, so an empty tensor never
+  // shifts a tensor into two launches.
+  for (int32_t j = 0; j < n;) {
     AdamJobs jobs;
     memset(&jobs, 0, sizeof(jobs));
     int64_t blocks = 0;
-    for (int32_t j = j0; j < n && jobs.n < kAdamMaxJobs; ++j) {
+    for (; j < n && jobs.n < kAdamMaxJobs; ++j) {
       if (numel[j] == 0) continue;
       AdamJob& J = jobs.job[jobs.n++];
       J.p = p[j]; J.g = g[j]; J.m = m[j]; J.v = v[j]; J.shadow = shadow ? (bf16_t*)shadow[j] : nullptr;

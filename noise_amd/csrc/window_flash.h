@@ -52,8 +52,8 @@ struct FlashArgs {
   float* lse_out;       // kAttn / kLse: [batch * heads, T] (optional for kAttn)
   float* xb_out;        // kAttn (optional): [batch, T, heads] = out_o . xb_vec[h*64 ..] (rank-1 partial dots)
   const float* xb_vec;  // kAttn: per-batch vector base, batch b uses xb_vec + xb_row[b] * xb_stride
-  const int32_t* xb_row;
-  int64_t xb_stride;
+  const int32_t* xb_row;  // entries outside [0, xb_rows) read row 0 (the forward marks such a member's loss NaN)
+  int64_t xb_stride, xb_rows;
   int32_t heads, T, window;
   // kAttn: the direct draws' jitter of the output (jit_sigma 0: none). Batch entry b is draw jit_draw0 + b / jit_n_seq
   // of token row jit_seq[b]; the jitter of output o, channel c of the heads * 64 comes from rng.h dust_noise_quad.
@@ -570,7 +570,11 @@ __global__ __launch_bounds__(256, (kFlashOccupancy<MODE, OPT>)) void window_flas
         static_assert(4 * 32 * 64 <= 2 * 64 * 64, "4 waves' staged tiles fit the input-tile LDS");
         bf16_t* y_stage = &ys[0][0] + wave * 2048;
         float dot = 0.f;
-        const float* bv = a.xb_out ? a.xb_vec + (int64_t)a.xb_row[b] * a.xb_stride + head * 64 : nullptr;
+        const float* bv = nullptr;
+        if (a.xb_out) {
+          const int32_t xr = a.xb_row[b];
+          bv = a.xb_vec + ((uint32_t)xr < (uint64_t)a.xb_rows ? (int64_t)xr : 0) * a.xb_stride + head * 64;
+        }
         const bool jit = a.jit_sigma != 0.f;
         const uint32_t jrow = jit ? (uint32_t)((int64_t)a.jit_seq[b] * T + my_o) : 0u;
         const uint32_t jdraw = jit ? (uint32_t)(a.jit_draw0 + b / a.jit_n_seq) : 0u;

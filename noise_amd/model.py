@@ -272,7 +272,8 @@ class GPT(nn.Module):
             tg = tg.contiguous()
         from .population import run_forward
         out = run_forward(self, idx.contiguous(), tg, member_seq=torch.arange(B, device=idx.device, dtype=torch.int32),
-                          noise=None, want_logits=targets is None, want_tokens=loss_reduction == 'none')
+                          noise=None, want_logits=targets is None, want_tokens=loss_reduction == 'none',
+                          check_tables=False)
         if targets is None:
             return out['logits'].view(B, Tp, -1)[:, :T]
         if loss_reduction == 'none':

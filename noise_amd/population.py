@@ -46,6 +46,7 @@ class NoiseLayout:
         s = _lib.NoisePerturbation()
         s.rows = None if rows is None else rows.data_ptr()
         s.stride = self.stride
+        s.n_rows = 0 if rows is None else rows.shape[0]
         s.resid_lambdas, s.x0_lambdas = self.col('resid_lambdas'), self.col('x0_lambdas')
         s.wte, s.lm_head = self.col('transformer.wte.weight'), self.col('lm_head.weight')
         for i in range(n_layer):
@@ -75,11 +76,47 @@ def workspace(device, nbytes):
     return buf
 
 
+def _check_tables(tokens, targets, member_seq, noise, member_row, member_sign, layout, dev, values):
+    """The member tables and token rows as the kernels read them: device, dtype, contiguity and sizes always; with
+    values, also every member_seq in [0, n_seq) and member_row in [0, n_rows) (a device-to-host sync). The kernels
+    guard the same ranges themselves (an out-of-range member's loss is NaN), so callers that build the tables
+    themselves skip the sync."""
+    if tokens.dim() != 2 or tokens.dtype != torch.int64 or not tokens.is_contiguous():
+        raise ValueError(f'tokens must be contiguous int64 [n_seq, T], got {tokens.dtype} {tuple(tokens.shape)}')
+    if targets is not None and (targets.shape != tokens.shape or targets.dtype != torch.int64
+                                or not targets.is_contiguous()):
+        raise ValueError('targets must be contiguous int64 of the tokens\' shape')
+    members = member_seq.numel()
+    tables = [('member_seq', member_seq, torch.int32)]
+    if noise is not None:
+        if noise.dim() != 2 or noise.dtype != torch.float32 or not noise.is_contiguous() or \
+                noise.shape[1] != layout.stride:
+            raise ValueError(f'noise must be contiguous fp32 [n_rows, {layout.stride}], got {noise.dtype} '
+                             f'{tuple(noise.shape)}')
+        tables += [('member_row', member_row, torch.int32), ('member_sign', member_sign, torch.float32)]
+    for name, t, dt in tables:
+        if t is None or t.dtype != dt or t.dim() != 1 or t.numel() != members or not t.is_contiguous():
+            raise ValueError(f'{name} must be contiguous {dt} [{members}]')
+    for name, t in [('tokens', tokens), ('targets', targets), ('noise', noise)] + [(n, t) for n, t, _ in tables]:
+        if t is not None and t.device != dev:
+            raise ValueError(f'{name} is on {t.device}, the model on {dev}')
+    if values:
+        checks = [('member_seq', member_seq, tokens.shape[0])]
+        if noise is not None:
+            checks.append(('member_row', member_row, noise.shape[0]))
+        for name, t, n in checks:
+            lo, hi = int(t.min()), int(t.max())
+            if lo < 0 or hi >= n:
+                raise ValueError(f'{name} holds entries in [{lo}, {hi}], outside [0, {n})')
+
+
 def run_forward(model, tokens, targets, member_seq, noise=None, member_row=None, member_sign=None, layout=None,
-                want_logits=False, want_tokens=False, want_sum=True):
+                want_logits=False, want_tokens=False, want_sum=True, check_tables=True):
     """One call of noise_population_forward: members evaluate rows of tokens [n_seq, T] (T % 128 == 0).
 
-    noise: fp32 rows [n_rows, layout.stride] or None; member_row / member_sign: int32 / fp32 [members]."""
+    noise: fp32 rows [n_rows, layout.stride] or None; member_row / member_sign: int32 / fp32 [members].
+    check_tables: also check the table entries' ranges on the host (a sync); callers that build their own tables
+    pass False (the kernels still turn an out-of-range member into a NaN loss)."""
     s, keep, dev = model.packed()
     n_seq, T = tokens.shape
     members = member_seq.numel()
@@ -89,6 +126,7 @@ def run_forward(model, tokens, targets, member_seq, noise=None, member_row=None,
     if noise is None:
         member_row = torch.zeros(members, dtype=torch.int32, device=dev)
         member_sign = torch.zeros(members, dtype=torch.float32, device=dev)
+    _check_tables(tokens, targets, member_seq, noise, member_row, member_sign, layout, dev, check_tables)
     pert = layout.struct(noise, model.config.n_layer)
     out = {}
     out['loss_sum'] = torch.empty(members, dtype=torch.float32, device=dev) if (targets is not None and want_sum) else None
@@ -201,7 +239,8 @@ def population_loss(model, p, noise, sign, idx, targets):
     tg = torch.nn.functional.pad(targets.to(torch.int64), (0, Tp - T), value=-1).view(1, Tp).contiguous()
     out = run_forward(model, tok, tg, member_seq=torch.zeros(m, dtype=torch.int32, device=dev), noise=rows,
                       member_row=torch.arange(m, dtype=torch.int32, device=dev),
-                      member_sign=sign.to(device=dev, dtype=torch.float32).contiguous(), layout=layout)
+                      member_sign=sign.to(device=dev, dtype=torch.float32).contiguous(), layout=layout,
+                      check_tables=False)
     return out['loss_sum'] / T
 
 
@@ -285,7 +324,7 @@ class Eggroll:
             local = torch.arange(dirs.numel(), device=self.device, dtype=torch.int32) // 2
             out = run_forward(self.model, tokens, targets, member_seq=seq[sl].to(torch.int32).contiguous(),
                               noise=rows, member_row=local, member_sign=(sgn[sl] * self.sigma).float().contiguous(),
-                              layout=self.layout)
+                              layout=self.layout, check_tables=False)
             losses[sl] = out['loss_sum'] / T
         if self.world > 1:
             gathered = [torch.empty_like(losses) for _ in range(self.world)]

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_lib.EXPORTS)
-    assert lib.noise_abi_version() == 3
+    assert lib.noise_abi_version() == 4 == _lib.ABI_VERSION
 
 
 def test_argument_errors_raise_before_any_gpu_call():
@@ -60,6 +60,45 @@ def test_credit_operands_must_match_q():
         credit.raw_value_credits(q, q, torch.zeros(2, 128), torch.zeros(1, 128, 64), 10)
     with pytest.raises(ValueError, match='values'):
         credit.key_context(q, q, torch.zeros(2, 128, 32), q, 10)
+
+
+def test_member_tables_are_checked_on_the_host():
+    """run_forward's host checks (noise_amd.population._check_tables): dtype, shape, contiguity and device always;
+    with values, entry ranges: member_seq in [0, n_seq) and member_row in [0, n_rows). The kernels guard the same
+    ranges on the device (an out-of-range member's loss is NaN), which the GPU tests cover."""
+    from noise_amd.population import _check_tables
+
+    class Lay:
+        stride = 10
+    cpu = torch.device('cpu')
+    tok = torch.zeros(2, 128, dtype=torch.int64)
+    rows = torch.zeros(3, 10)
+    seq = torch.tensor([0, 1, 0, 1], dtype=torch.int32)
+    row = torch.tensor([0, 0, 2, 2], dtype=torch.int32)
+    sign = torch.zeros(4)
+    _check_tables(tok, tok, seq, rows, row, sign, Lay, cpu, True)
+    _check_tables(tok, None, seq, None, None, None, Lay, cpu, True)
+    cases = [
+        (dict(seq=torch.tensor([0, 1, 2, 1], dtype=torch.int32)), 'member_seq holds'),
+        (dict(seq=torch.tensor([0, -1, 0, 1], dtype=torch.int32)), 'member_seq holds'),
+        (dict(row=torch.tensor([0, 0, 3, 2], dtype=torch.int32)), 'member_row holds'),
+        (dict(row=torch.tensor([0, 0, 2], dtype=torch.int32)), 'member_row must be'),
+        (dict(row=row.long()), 'member_row must be'),
+        (dict(sign=torch.zeros(4, dtype=torch.float64)), 'member_sign must be'),
+        (dict(seq=seq.long()), 'member_seq must be'),
+        (dict(rows=torch.zeros(3, 9)), 'noise must be'),
+        (dict(tok=tok.int()), 'tokens must be'),
+        (dict(tg=tok[:, :64]), 'targets must be'),
+    ]
+    for change, msg in cases:
+        a = dict(tok=tok, tg=tok, seq=seq, rows=rows, row=row, sign=sign)
+        a.update(change)
+        with pytest.raises(ValueError, match=msg):
+            _check_tables(a['tok'], a['tg'], a['seq'], a['rows'], a['row'], a['sign'], Lay, cpu, True)
+    # ranges are only checked with values (the kernels guard them on the device)
+    _check_tables(tok, tok, torch.tensor([0, 1, 5, 1], dtype=torch.int32), rows, row, sign, Lay, cpu, False)
+    with pytest.raises(ValueError, match='the model on meta'):
+        _check_tables(tok, tok, seq, rows, row, sign, Lay, torch.device('meta'), False)
 
 
 def test_compute_on_cpu_tensors_is_refused():

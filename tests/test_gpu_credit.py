@@ -50,19 +50,25 @@ def test_lse_and_value_pass(dev, T, window, unit):
 
 
 @pytest.mark.parametrize('T,window,unit,scale', [(256, 256, True, 1.0), (384, 128, False, 1.0), (2048, 1024, True, 1.0),
-                                                  (2048, 2048, False, 1.0), (256, 100, True, 2.5)])
+                                                  (2048, 2048, False, 1.0), (256, 100, True, 1.8),
+                                                  (2048, 2048, True, 'aligned')])
 def test_lse_bounded(dev, T, window, unit, scale):
-    """The bounded LSE pass (no running maximum; the caller's |q . k| / 8 <= 80) against the oracle and against the
+    """The bounded LSE pass (no running maximum; the caller's |q . k| / 8 <= 16) against the oracle and against the
     running-maximum pass. It rounds q log2(e) / 8 to bf16 once more, an error that grows with the logit: within
-    2e-2 + 2e-3 max|logit| absolute. scale 2.5 puts logits up to about 50 (6.25 times the RMS-normed bound)."""
+    2e-2 + 2e-3 max|logit| absolute. scale 1.8 puts logits up to about 15; 'aligned' sets k = q with |q|^2 = 128, so
+    every query's own key sits exactly at the documented bound of 16, over the full 2048-wide window."""
     from noise_amd import credit
     print(f'credit lse bounded T={T} window={window} unit={unit} scale={scale}', flush=True)
     rows = 2 if T > 1024 else 3
     q, k = _qk(rows, T, unit, seed=T + 7 * window)
-    q = (q.float() * scale).bfloat16()
-    k = (k.float() * scale).bfloat16()
+    if scale == 'aligned':
+        q = (q.float() * 2 ** 0.5).bfloat16()
+        k = q.clone()
+    else:
+        q = (q.float() * scale).bfloat16()
+        k = (k.float() * scale).bfloat16()
     big = (q.float() @ k.float().transpose(1, 2)).abs().max().item() / 8
-    assert big <= 80
+    assert big <= 16.5  # the bf16 rounding of |q|^2 = 128 may land just past 16
     tol = 2e-2 + 2e-3 * big
     lse_ref = oc.lse(q.float(), k.float(), window)
     got = credit.credit_lse(q.to(dev), k.to(dev), window, bounded=True).cpu()

@@ -215,3 +215,39 @@ def test_hooked_forward_runs_module_by_module(dev):
         for h in hooks:
             h.remove()
     assert torch.equal(model(idx.to(dev), tg.to(dev), loss_reduction='none').cpu(), fused)  # fused again
+
+
+def test_out_of_range_member_tables_give_nan_for_that_member_only(dev):
+    """member_seq and member_row are read on the device. One member with member_row = n_rows and one with
+    member_seq = -1 (passed past the host check): each gets a NaN loss (every token NaN), reads nothing out of range,
+    and every other member's loss is bit-identical to the call with valid tables. The host check rejects both."""
+    from noise_amd.population import Eggroll, NoiseLayout, run_forward
+    print('population forward with out-of-range member tables m=6 T=256', flush=True)
+    ocfg, gcfg = _cfgs()
+    model = _model(dev, _weights(ocfg), gcfg)
+    layout = NoiseLayout(model)
+    es = Eggroll(model, 3, sigma=0.01, seed=5, chunk=3)
+    rows = es.rows(es.offset_table(2), torch.arange(3, device=dev))
+    idx, tg = recipe.tokens(ocfg, batch=2, seed=13)
+    idx, tg = idx.to(dev), tg.to(dev)
+    seq = torch.tensor([0, 1, 0, 1, 0, 1], dtype=torch.int32, device=dev)
+    row = torch.tensor([0, 0, 1, 1, 2, 2], dtype=torch.int32, device=dev)
+    sign = torch.tensor([0.01, -0.01] * 3, device=dev)
+    good = run_forward(model, idx, tg, seq, noise=rows, member_row=row, member_sign=sign, layout=layout,
+                       want_tokens=True)
+    bad_seq, bad_row = seq.clone(), row.clone()
+    bad_row[2] = 3          # one past the 3 noise rows
+    bad_seq[5] = -1
+    with pytest.raises(ValueError, match='member_row'):
+        run_forward(model, idx, tg, seq, noise=rows, member_row=bad_row, member_sign=sign, layout=layout)
+    with pytest.raises(ValueError, match='member_seq'):
+        run_forward(model, idx, tg, bad_seq, noise=rows, member_row=row, member_sign=sign, layout=layout)
+    out = run_forward(model, idx, tg, bad_seq, noise=rows, member_row=bad_row, member_sign=sign, layout=layout,
+                      want_tokens=True, check_tables=False)
+    loss, tok = out['loss_sum'].cpu(), out['token_loss'].cpu().view(6, -1)
+    want, want_tok = good['loss_sum'].cpu(), good['token_loss'].cpu().view(6, -1)
+    assert torch.isnan(loss[2]) and torch.isnan(loss[5]), loss
+    assert torch.isnan(tok[2]).all() and torch.isnan(tok[5]).all()
+    ok = [0, 1, 3, 4]
+    assert torch.isfinite(want).all()
+    assert torch.equal(loss[ok], want[ok]) and torch.equal(tok[ok], want_tok[ok])

@@ -57,29 +57,72 @@ def test_config1_gpt_forward_t2048(dev):
     assert ((logits - lref).abs().max() / lref.abs().max()).item() < 2e-2
 
 
-def test_config4_population_t2048(dev):
-    """Config 4's per-member losses: 8 members (4 antithetic pairs) at the production sigma 0.002 on one 2048-token
-    sequence, every parameter perturbed. Also the pair differences (the fitness signal) against the oracle's."""
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize('members', [8, 64])
+def test_config4_population_t2048(dev, members):
+    """Config 4's per-member losses: 8 members (4 antithetic pairs), and 64 (32 pairs), at the production sigma 0.002
+    on one 2048-token sequence, every parameter perturbed. Also the pair differences (the fitness signal) against the
+    oracle's: correlated, and off by at most 5% of their mean magnitude on average (measured: 0.3-0.6%). A sign or
+    slice mistake in one small parameter's rank-1 term moves the differences by a few percent. The oracle runs in
+    chunks of 8 members (its attention holds [members, heads, T, T] scores)."""
     from noise_amd.population import population_loss
-    print('config 4: population loss m=8 T=2048 sigma=0.002', flush=True)
+    print(f'config 4: population loss m={members} T=2048 sigma=0.002', flush=True)
     ocfg = om.Config()
     w = _weights()
     model = _model(dev, w)
-    members, sigma = 8, 0.002
+    sigma = 0.002
     noise = recipe.population_noise(ocfg, members, seed=77, step=2)
     sign = torch.tensor([sigma, -sigma] * (members // 2))
     idx, tg = recipe.tokens(ocfg, batch=1, seed=31)
-    ref = om.population_loss(w, ocfg, noise, sign, idx[0], tg[0]) / ocfg.sequence_len
+    ref = []
+    for c in range(0, members, 8):
+        part = {k: tuple(t[c:c + 8] for t in v) if isinstance(v, tuple) else v[c:c + 8] for k, v in noise.items()}
+        ref.append(om.population_loss(w, ocfg, part, sign[c:c + 8], idx[0], tg[0]) / ocfg.sequence_len)
+        print(f'oracle members {c}..{c + 7} done', flush=True)
+    ref = torch.cat(ref)
     dnoise = {k: tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for k, v in noise.items()}
     got = population_loss(model, None, dnoise, sign.to(dev), idx[0].to(dev), tg[0].to(dev)).cpu()
     rel = ((got - ref).abs() / ref.abs()).max().item()
     d_ref, d_got = (ref[1::2] - ref[0::2]).double(), (got[1::2] - got[0::2]).double()
     corr = np.corrcoef(d_ref.numpy(), d_got.numpy())[0, 1]
     derr = ((d_got - d_ref).abs().mean() / d_ref.abs().mean()).item()
-    print(f'member max rel err {rel:.3e}; pair differences oracle {d_ref.tolist()} gpu {d_got.tolist()}; '
-          f'correlation {corr:.4f}; mean |error| / mean |difference| {derr:.3f}', flush=True)
+    print(f'member max rel err {rel:.3e}; pair differences oracle {d_ref.tolist()[:8]} gpu {d_got.tolist()[:8]}; '
+          f'correlation {corr:.5f}; mean |error| / mean |difference| {derr:.4f}', flush=True)
     assert rel < 1e-2, (got, ref)
-    assert corr > 0.95 and derr < 0.2, (corr, derr)
+    assert corr > (0.95 if members == 8 else 0.99) and derr < 0.05, (corr, derr)
+
+
+def test_config4_population_12_layers_t2048(dev):
+    """BASELINE.json's configs[3] read literally: the 12-layer model (GPTConfig n_layer=12; 54.5M parameters) through
+    the same population forward, 8 members (4 pairs) at sigma 0.002 on one 2048-token sequence, per-member losses
+    within 1e-2 of the oracle's 12-layer population loss and the pair differences within 5% on average."""
+    from noise_amd.model import GPT, GPTConfig
+    from noise_amd.population import population_loss
+    print('config 4 at 12 layers: population loss m=8 T=2048 sigma=0.002', flush=True)
+    ocfg = om.Config(n_layer=12)
+    w = recipe.weights(ocfg, seed=97)
+    with torch.device('meta'):
+        model = GPT(GPTConfig(n_layer=12))
+    model.to_empty(device=dev)
+    model.init_weights()
+    model.transformer.wte.float()
+    for e in model.value_embeds.values():
+        e.float()
+    model.load_state_dict({k: v.to(dev) for k, v in w.items()}, strict=True)
+    members, sigma = 8, 0.002
+    noise = recipe.population_noise(ocfg, members, seed=79, step=4)
+    sign = torch.tensor([sigma, -sigma] * (members // 2))
+    idx, tg = recipe.tokens(ocfg, batch=1, seed=37)
+    ref = om.population_loss(w, ocfg, noise, sign, idx[0], tg[0]) / ocfg.sequence_len
+    dnoise = {k: tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for k, v in noise.items()}
+    got = population_loss(model, None, dnoise, sign.to(dev), idx[0].to(dev), tg[0].to(dev)).cpu()
+    rel = ((got - ref).abs() / ref.abs()).max().item()
+    d_ref, d_got = (ref[1::2] - ref[0::2]).double(), (got[1::2] - got[0::2]).double()
+    derr = ((d_got - d_ref).abs().mean() / d_ref.abs().mean()).item()
+    print(f'12 layers: member max rel err {rel:.3e}; pair differences oracle {d_ref.tolist()} gpu {d_got.tolist()}; '
+          f'mean |error| / mean |difference| {derr:.4f}', flush=True)
+    assert rel < 1e-2, (got, ref)
+    assert derr < 0.05, derr
 
 
 @pytest.mark.parametrize('window', [2048, 1024])

@@ -42,7 +42,7 @@ def test_population_forward_and_credit_replay_bit_for_bit(dev):
 
     def work():
         out = run_forward(model, idx, tg, member_seq, noise=rows, member_row=member_row, member_sign=member_sign,
-                          layout=layout, want_tokens=True)
+                          layout=layout, want_tokens=True, check_tables=False)  # no host sync under capture
         return out['loss_sum'], out['token_loss'], credit.value_credit(q, k, e, 128)
 
     eager = [t.clone() for t in work()]

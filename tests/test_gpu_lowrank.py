@@ -82,4 +82,4 @@ def test_shared_sumsq_config2(dev):
             err = (s[i] - want[j]).abs().item()
             print(f'{md} member {i}: S {s[i].item():.6e} oracle {want[j].item():.6e} member part {part:.4e} '
                   f'err {err:.3e}', flush=True)
-            assert err < 1e-2 * part, (md, i, err, part)
+            assert err < 1e-3 * part, (md, i, err, part)  # measured 2.4e-5 of the member part

@@ -150,6 +150,31 @@ def test_adamw_groups_weight_decay_and_skipped_steps_match_torch(dev):
     assert opt.state[mine[0][1]]['step'] == 3 and opt.state[mine[0][0]]['step'] == 4
 
 
+def test_adamw_batch_many_tensors_with_empty_ones_match_torch(dev):
+    """More tensors than one launch takes (48), with empty tensors among them (two inside the first 48, one at the
+    start of the second launch's range, one last): every tensor must take exactly one step per call, so the result
+    equals torch.optim.AdamW after 3 steps. A tensor stepped twice (the batching's cursor restarting behind the last
+    tensor it took) would differ by a whole Adam step."""
+    from noise_amd.optim import AdamW
+    g = torch.Generator().manual_seed(11)
+    sizes = [int(s) for s in torch.randint(1, 300, (60,), generator=g)]
+    for j in (3, 20, 48, 59):
+        sizes[j] = 0
+    init = [torch.randn(n, generator=g) for n in sizes]
+    ref = [torch.nn.Parameter(t.clone()) for t in init]
+    mine = [torch.nn.Parameter(t.clone().to(dev)) for t in init]
+    opt_ref = torch.optim.AdamW(ref, lr=1e-2, betas=(0.8, 0.95), eps=1e-8, weight_decay=0.1)
+    opt = AdamW(mine, lr=1e-2, betas=(0.8, 0.95), eps=1e-8, weight_decay=0.1)
+    for _ in range(3):
+        for r, m, n in zip(ref, mine, sizes):
+            grad = torch.randn(n, generator=g)
+            r.grad, m.grad = grad.clone(), grad.to(dev)
+        opt_ref.step()
+        opt.step()
+    for j, (r, m) in enumerate(zip(ref, mine)):
+        assert torch.allclose(m.detach().cpu(), r.detach(), rtol=1e-5, atol=1e-7), (j, sizes[j])
+
+
 def test_eggroll_step_decomposed(dev):
     """One Eggroll.step on a 256-token model: losses vs the oracle's population forward, fitness from those losses,
     and the gradient the oracle assembles from the GPU's own direction weights."""

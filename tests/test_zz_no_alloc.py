@@ -68,3 +68,57 @@ def test_static_entry_point_rejects_sizes_past_its_array(dev):
         _run(_lib.call, 'noise_lowrank_static', dev, x, 1, W, rows, sign, T, n_in, n_out, m)
     with pytest.raises(ValueError, match='x_shared 1 or 2'):
         _run(_lib.call, 'noise_lowrank_static', dev, x, 0, W, rows, sign, T, n_in, n_out, m)
+
+
+def _capture_and_check(dev, T, n_in, n_out, m, seed, eager_first):
+    """Captures noise_lowrank_static into a HIP graph on torch's capture stream (a side stream), replays it three
+    times with eager work and synchronizations between the replays, and holds every replay bit-equal to
+    noise_lowrank's result on the same inputs. eager_first: noise_lowrank (and so the kernels' one-time attribute
+    set-up) runs before the capture; otherwise the static entry point's first call on the device, with its scratch
+    address lookup, is the captured one."""
+    from noise_amd import _lib
+    lib = _lib.lib()
+    x, W, rows, sign = _inputs(dev, T, n_in, n_out, m, seed=seed)
+    ws = torch.empty(lib.noise_lowrank_workspace(m, T, n_in, n_out, 1), dtype=torch.uint8, device=dev)
+    want = None
+    if eager_first:
+        want = _run(_lib.call, 'noise_lowrank', dev, x, 1, W, rows, sign, T, n_in, n_out, m, ws=ws)
+    torch.cuda.synchronize()
+    out = torch.full((m,), float('nan'), device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.call('noise_lowrank_static', _lib.ptr(x), 1, _lib.ptr(W), _lib.ptr(rows), rows.shape[1], 3, 3 + n_out,
+                  _lib.ptr(sign), m, T, n_in, n_out, None, _lib.ptr(out), _lib.stream(dev))
+    if want is None:
+        want = _run(_lib.call, 'noise_lowrank', dev, x, 1, W, rows, sign, T, n_in, n_out, m, ws=ws)
+    torch.cuda.synchronize()
+    assert torch.isfinite(want).all()
+    for rep in range(3):
+        out.fill_(float('nan'))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), (rep, (out - want).abs().max().item())
+        x2, W2, r2, s2 = _inputs(dev, 1024, 128, 512, 9, seed=rep)  # eager use of the same scratch in between
+        _run(_lib.call, 'noise_lowrank_static', dev, x2, 1, W2, r2, s2, 1024, 128, 512, 9)
+        torch.cuda.synchronize()
+
+
+def test_static_entry_point_replays_under_graph_capture(dev):
+    print('noise_lowrank_static under graph capture, after eager calls', flush=True)
+    _capture_and_check(dev, 4096, 512, 2048, 64, seed=31, eager_first=True)
+
+
+def test_static_entry_point_first_call_under_graph_capture():
+    """The same in a fresh process whose first call of the library on the device is the captured one."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    if not torch.cuda.is_available():
+        pytest.skip('no GPU')
+    root = Path(__file__).resolve().parents[1]
+    code = ('import sys, torch; sys.path.insert(0, %r); from tests import test_zz_no_alloc as t; '
+            't._capture_and_check(torch.device("cuda", 0), 2048, 512, 1024, 32, seed=37, eager_first=False); '
+            'print("ok", flush=True)' % str(root))
+    print('noise_lowrank_static first call under graph capture, fresh process', flush=True)
+    r = subprocess.run([sys.executable, '-c', code], cwd=str(root), capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith('ok'), (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
