@@ -252,6 +252,48 @@ def bench_c5(args, dev, steps=None, warmup=None):
     return res
 
 
+def bench_hooked_forward(dev, model, iters=5):
+    """GPT.forward (utils/model.py:193-210) on an 8 x 2048 Zipf(1.1) batch two ways: the fused population forward
+    (one unperturbed member per sequence), and module by module, as it runs when a caller hooks submodules
+    (train/val/dust.py:166-168): the linears on noise_linear, the attention on the flash kernel, torch's elementwise
+    ops under bf16 autocast. Each a median of `iters` timed calls after one warmup, no autograd."""
+    import torch
+    from noise_amd import _lib
+    x, y = zipf_tokens(8, T_SEQ, seed=3)
+    x, y = x.to(dev), y.to(dev)
+    out = {}
+    for name, hooked in (('fused', False), ('hooked', True)):
+        h = model.lm_head.register_forward_hook(lambda *a: None) if hooked else None
+        try:
+            with torch.no_grad():
+                model(x, y)
+                torch.cuda.synchronize()
+                _lib.timing_enable(True)
+                times = []
+                for _ in range(iters):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    loss = model(x, y)
+                    e1.record()
+                    torch.cuda.synchronize()
+                    times.append(e0.elapsed_time(e1))
+                tm = _lib.timing_read()
+                _lib.timing_enable(False)
+        finally:
+            if h is not None:
+                h.remove()
+        ms = statistics.median(times)
+        out[name] = dict(ms=round(ms, 3), tokens_per_s=round(8 * T_SEQ / (ms * 1e-3), 1),
+                         loss=round(float(loss), 4))
+        if hooked:
+            n, lin_ms = tm.get('linear', (0, 0.0))
+            out[name]['linear_launches_per_call'] = n // iters
+            out[name]['linear_ms_per_call'] = round(lin_ms / iters, 3)
+    out['note'] = ('8 x 2048 tokens, no perturbation; hooked: a no-op forward hook on lm_head sends GPT.forward '
+                   'module by module (the reference\'s call sequence), its linears on noise_linear')
+    return out
+
+
 def c4_12layer_record(dev, steps=5, warmup=1):
     """BASELINE.json's configs[3] read literally: the config-4 population forward on the 12-layer model (GPTConfig
     n_layer=12, 54.5M parameters; windows SSSL repeated, value embeddings on alternate layers), same members, tokens
@@ -323,6 +365,21 @@ def bench_credit(dev, iters=10):
             else:
                 out[f'window_{window}'].update(hi_lo_value_ms=round(val_ms, 4),
                                                hi_lo_tflops=round(flops / ((lse_ms + val_ms) * 1e-3) / 1e12, 1))
+        # the general readout: the LSE pass with its running maximum (no bound on the logits, as the reference's
+        # kernels), then the same value pass
+        for _ in range(2):
+            credit.value_credit(q, k, e, window, hi_lo=False, bounded=False)
+        torch.cuda.synchronize()
+        _lib.timing_enable(True)
+        for _ in range(iters):
+            credit.value_credit(q, k, e, window, hi_lo=False, bounded=False)
+        torch.cuda.synchronize()
+        tm = _lib.timing_read()
+        _lib.timing_enable(False)
+        rm_lse = tm['credit_lse'][1] / tm['credit_lse'][0]
+        rm_val = tm['credit_value'][1] / tm['credit_value'][0]
+        out[f'window_{window}'].update(running_max_lse_ms=round(rm_lse, 4), running_max_value_ms=round(rm_val, 4),
+                                       running_max_tflops=round(flops / ((rm_lse + rm_val) * 1e-3) / 1e12, 1))
         # the key-context pass (lse and center): q.k and hub.v dots, 4d FLOPs per pair
         vals = (torch.randn(rows, T, 64, device=dev, generator=g)).bfloat16()
         hub = e.bfloat16()
@@ -724,6 +781,7 @@ def main():
         line['c5'] = c5_record(dev)
     if args.workload == 'c4':
         line['c4_12layer'] = c4_12layer_record(dev)
+        line['gpt_forward'] = bench_hooked_forward(dev, model)
     if not args.no_dust:
         line['dust_head_error'] = bench_head_error(dev)
         line['dust_direct'] = bench_dust_direct(dev, model)

@@ -88,6 +88,15 @@ int noise_lowrank_embed(const void* w, int32_t w_bf16, int64_t vocab, int32_t d,
                         const float* b, int64_t b_stride, const int64_t* idx, const float* sign, int32_t m, int64_t T,
                         float* out, void* stream);
 
+/* The unperturbed bf16 linear of the module-by-module forward: y[r, :] = bf16(x[r, :] W^T) with fp32 accumulation,
+ * x bf16 [M, in] (row stride ldx), W bf16 [out, in] (nn.Linear's weight), y bf16 [M, out] (row stride ldy).
+ * in % 32 == 0, out % 256 == 0, ldx % 8 == 0, ldy % 4 == 0; x and W 16-byte aligned, y 8-byte aligned.
+ * Replaces: torch.nn.Linear.forward under bf16 autocast (F.linear) for the c_q, c_k, c_v, c_proj, c_fc and lm_head
+ * modules of utils/model.py:69-79, 100-104, 138 when GPT.forward runs module by module (hooked callers such as
+ * train/val/dust.py:166-168). */
+int noise_linear(const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M, int64_t in, int64_t out, uint16_t* y,
+                 int64_t ldy, void* stream);
+
 /* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): noise_lowrank's shared-x path (x_shared 1 or 2, same
  * arguments, results bit-identical to noise_lowrank's) with its workspace in a static device array of

@@ -11,7 +11,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load order: torch's HIP runtime first)
 
 LIB_PATH = Path(__file__).resolve().parent / 'libnoise_amd.so'
-ABI_VERSION = 4  # include/noise_amd.h's signatures (noise_abi_version)
+ABI_VERSION = 5  # include/noise_amd.h's signatures (noise_abi_version)
 MAX_LAYERS = 16
 
 c_p = ctypes.c_void_p
@@ -52,6 +52,7 @@ _SIGNATURES = {
     'noise_lowrank': ([c_p, i32, c_p, c_p, i64, i64, i64, c_p, i64, i64, i64, i64, c_p, c_p, c_p, szt, c_p],
                       ctypes.c_int),
     'noise_lowrank_workspace': ([i64, i64, i64, i64, i32], szt),
+    'noise_linear': ([c_p, i64, c_p, i64, i64, i64, c_p, i64, c_p], ctypes.c_int),
     'noise_lowrank_static': ([c_p, i32, c_p, c_p, i64, i64, i64, c_p, i64, i64, i64, i64, c_p, c_p, c_p], ctypes.c_int),
     'noise_attention': ([c_p, c_p, c_p, i64, i32, i64, i64, i64, i32, c_p, i64, i64, c_p, c_p], ctypes.c_int),
     'noise_population_forward_workspace': ([i64, i64], szt),

@@ -19,7 +19,7 @@ int noise_set_error(int code, const char* fmt, ...) {
 
 extern "C" const char* noise_last_error(void) { return g_error; }
 
-extern "C" int noise_abi_version(void) { return 4; }
+extern "C" int noise_abi_version(void) { return 5; }
 
 // ---- timing -----------------------------------------------------------------------------------------------------
 namespace {
@@ -32,7 +32,7 @@ const char* kNames[kTimeClasses] = {"noise", "embed", "norm", "qkv_gemm", "rope_
                                     "fc_gemm", "rowdot", "mlp_proj_gemm", "head_ce_gemm", "ce_finalize", "credit_lse",
                                     "credit_value", "outer_grad", "lowrank_gemm", "credit_center",
                                     "head_error", "dust_rerun", "dust_errors", "lowrank_pre", "lowrank_post", "fitness", "vector_grad", "adamw",
-                                    "reassemble"};
+                                    "reassemble", "linear"};
 int64_t g_count[kTimeClasses];
 double g_ms[kTimeClasses];
 

@@ -204,7 +204,8 @@ int noise_set_error(int code, const char* fmt, ...);
 enum NoiseTimingClass {
   kTimeNoise = 0, kTimeEmbed, kTimeNorm, kTimeQKV, kTimeRope, kTimeAttention, kTimeProj, kTimeFc, kTimeRowdot,
   kTimeMlpProj, kTimeHead, kTimeCeFinal, kTimeCreditLse, kTimeCreditValue, kTimeUpdate, kTimeLowrank, kTimeCreditCenter, kTimeHeadError, kTimeDustRerun, kTimeDustErrors,
-  kTimeLowrankPre, kTimeLowrankPost, kTimeFitness, kTimeVectorGrad, kTimeAdamw, kTimeReassemble, kTimeClasses
+  kTimeLowrankPre, kTimeLowrankPost, kTimeFitness, kTimeVectorGrad, kTimeAdamw, kTimeReassemble, kTimeLinear,
+  kTimeClasses
 };
 
 struct NoiseTimer {

@@ -586,6 +586,50 @@ extern "C" int noise_lowrank(const uint16_t* x, int32_t x_shared, const uint16_t
   return NOISE_OK;
 }
 
+// ---- the plain bf16 linear ----------------------------------------------------------------------------------------
+
+namespace noise {
+// y = bf16(x W^T) (the autocast rounding of the matmul output), stored as bf16; rows past M are not stored.
+struct EpiLinear {
+  bf16_t* y;
+  int64_t ldy;
+  int M;
+  static constexpr int kRows = kEpiRows;
+  struct Wave {};
+  struct Pre {};
+  __device__ __forceinline__ void begin(int, int, int, int, Wave&) const {}
+  __device__ __forceinline__ void load(int, int, int, const Wave&, Pre&) const {}
+  template <int R>
+  __device__ __forceinline__ void rows(int row0, int n0, int, int lane, const Wave&, const Pre&, f32x4 (&v)[R]) const {
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+      if (row0 + q < M)  // the staged values are already bf16: packing them is exact
+        __builtin_nontemporal_store((u32x2{pack_bf16x2(v[q][0], v[q][1]), pack_bf16x2(v[q][2], v[q][3])}),
+                                    (u32x2*)(y + (int64_t)(row0 + q) * ldy + n0 + 4 * lane));
+  }
+};
+using LinTile = GemmShape<128, 256, 32, 2, 2, 3, 2>;  // two workgroups per CU
+}  // namespace noise
+
+extern "C" int noise_linear(const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M, int64_t in, int64_t out,
+                            uint16_t* y, int64_t ldy, void* stream) {
+  NOISE_REQUIRE(x && w && y, "NULL pointer argument");
+  NOISE_REQUIRE(M > 0 && M <= (int64_t)INT32_MAX / 4, "M = %lld outside [1, 2^29)", (long long)M);
+  NOISE_REQUIRE(in > 0 && in % 32 == 0 && in <= 65536 && out > 0 && out % 256 == 0 && out <= 65536,
+                "in = %lld must be a multiple of 32 and out = %lld a multiple of 256", (long long)in, (long long)out);
+  NOISE_REQUIRE(ldx >= in && ldx % 8 == 0 && ldy >= out && ldy % 4 == 0,
+                "row strides: ldx >= in, a multiple of 8; ldy >= out, a multiple of 4");
+  NOISE_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)y & 7) == 0,
+                "x and w must be 16-byte aligned, y 8-byte aligned");
+  NOISE_REQUIRE((M + LinTile::BM - 1) / LinTile::BM <= 65535, "M too large for one launch");
+  NOISE_CHECK_HIP((prepare_gemm<LinTile, EpiLinear>()));
+  EpiLinear epi{(bf16_t*)y, ldy, (int)M};
+  NoiseTimer tm(kTimeLinear, (hipStream_t)stream);
+  NOISE_CHECK_HIP((launch_gemm<LinTile>((const bf16_t*)x, ldx, (const bf16_t*)w, in, (int)M, (int)out, (int)in, epi,
+                                         (hipStream_t)stream)));
+  return NOISE_OK;
+}
+
 // ---- the no-allocation variant of the shared-x path -------------------------------------------------------------
 
 // The workspace of noise_lowrank_static: a file-scope device array, one copy per GPU (held until the process ends).

@@ -64,6 +64,35 @@ def attention(q, k, v, window):
     return out[:, :T].to(dtype)
 
 
+def linear_bf16(x, weight):
+    """x @ weight.t() as bf16 autocast computes it (bf16 operands, fp32 accumulation, bf16 output) on the HIP GEMM
+    (noise_linear): x [..., in] on the GPU, weight [out, in] with in % 32 == 0 and out % 256 == 0."""
+    _lib.require_device(x, weight)
+    n_out, n_in = weight.shape
+    lead = x.shape[:-1]
+    xb = x.reshape(-1, n_in).to(torch.bfloat16).contiguous()
+    wb = weight.detach().to(torch.bfloat16).contiguous()
+    y = torch.empty(xb.shape[0], n_out, dtype=torch.bfloat16, device=x.device)
+    if xb.shape[0]:
+        _lib.call('noise_linear', _lib.ptr(xb), n_in, _lib.ptr(wb), xb.shape[0], n_in, n_out, _lib.ptr(y), n_out,
+                  _lib.stream(x.device))
+    return y.view(*lead, n_out)
+
+
+class Linear(nn.Linear):
+    """nn.Linear (same parameters and state-dict keys) whose bf16-autocast forward runs on the HIP GEMM: inside a
+    cuda bf16 autocast region, with no autograd graph to record, y = bf16(x W^T) comes from noise_linear, as
+    F.linear under autocast computes it. Elsewhere (fp32 calls, or a graph that needs gradients) it is nn.Linear."""
+
+    def forward(self, x):
+        if (x.is_cuda and self.bias is None and torch.is_autocast_enabled('cuda')
+                and torch.get_autocast_dtype('cuda') == torch.bfloat16
+                and self.in_features % 32 == 0 and self.out_features % 256 == 0
+                and not (torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad))):
+            return linear_bf16(x, self.weight)
+        return super().forward(x)
+
+
 class CausalSelfAttention(nn.Module):
     def __init__(self, config, layer_idx):
         super().__init__()
@@ -72,10 +101,10 @@ class CausalSelfAttention(nn.Module):
         self.n_embd = config.n_embd
         self.head_dim = self.n_embd // self.n_head
         assert self.n_embd % self.n_head == 0
-        self.c_q = nn.Linear(self.n_embd, self.n_head * self.head_dim, bias=False)
-        self.c_k = nn.Linear(self.n_embd, self.n_kv_head * self.head_dim, bias=False)
-        self.c_v = nn.Linear(self.n_embd, self.n_kv_head * self.head_dim, bias=False)
-        self.c_proj = nn.Linear(self.n_embd, self.n_embd, bias=False)
+        self.c_q = Linear(self.n_embd, self.n_head * self.head_dim, bias=False)
+        self.c_k = Linear(self.n_embd, self.n_kv_head * self.head_dim, bias=False)
+        self.c_v = Linear(self.n_embd, self.n_kv_head * self.head_dim, bias=False)
+        self.c_proj = Linear(self.n_embd, self.n_embd, bias=False)
         self.ve_gate_channels = 32
         self.ve_gate = (nn.Linear(self.ve_gate_channels, self.n_kv_head, bias=False)
                         if has_ve(layer_idx, config.n_layer) else None)
@@ -98,8 +127,8 @@ class CausalSelfAttention(nn.Module):
 class MLP(nn.Module):
     def __init__(self, config):
         super().__init__()
-        self.c_fc = nn.Linear(config.n_embd, 4 * config.n_embd, bias=False)
-        self.c_proj = nn.Linear(4 * config.n_embd, config.n_embd, bias=False)
+        self.c_fc = Linear(config.n_embd, 4 * config.n_embd, bias=False)
+        self.c_proj = Linear(4 * config.n_embd, config.n_embd, bias=False)
 
     def forward(self, x):
         """utils/model.py:106-107: c_proj(relu(c_fc(x))^2)."""
@@ -136,7 +165,7 @@ class GPT(nn.Module):
             'wte': nn.Embedding(padded_vocab, config.n_embd),
             'h': nn.ModuleList([Block(config, i) for i in range(config.n_layer)]),
         })
-        self.lm_head = nn.Linear(config.n_embd, padded_vocab, bias=False)
+        self.lm_head = Linear(config.n_embd, padded_vocab, bias=False)
         self.resid_lambdas = nn.Parameter(torch.ones(config.n_layer))
         self.x0_lambdas = nn.Parameter(torch.zeros(config.n_layer))
         head_dim = config.n_embd // config.n_head
@@ -286,8 +315,9 @@ class GPT(nn.Module):
         raise ValueError(f'unknown loss_reduction {loss_reduction!r}')
 
     def _forward_modules(self, idx, targets, loss_reduction):
-        """The module-by-module forward (utils/model.py:193-210's call sequence, which hooks observe): torch's bf16
-        linears and the HIP flash attention."""
+        """The module-by-module forward (utils/model.py:193-210's call sequence, which hooks observe): the bf16
+        linears on the HIP GEMM (Linear, noise_linear; the 32 -> 8 value-embedding gate on torch's), the HIP flash
+        attention, and torch's elementwise ops under bf16 autocast as the reference's."""
         B, T = idx.shape
         cos_sin = (self.cos[:, :T], self.sin[:, :T])
         with torch.autocast('cuda', dtype=torch.bfloat16):

@@ -37,30 +37,51 @@ class NoiseLayout:
             col += w
         self.stride = col
         self.index = {n: i for i, n in enumerate(self.names)}
-        self.widths_c = (ctypes.c_int64 * len(self.widths))(*self.widths)
+        self._widths_c = None
+
+    @property
+    def widths_c(self):
+        """The widths as a ctypes int64 array (built on first use: the constructor stays plain Python, which
+        torch.compile traces without a graph break)."""
+        if self._widths_c is None:
+            self._widths_c = (ctypes.c_int64 * len(self.widths))(*self.widths)
+        return self._widths_c
 
     def col(self, name):
         return self.col0[self.index[name]]
 
-    def struct(self, rows, n_layer):
-        s = _lib.NoisePerturbation()
-        s.rows = None if rows is None else rows.data_ptr()
-        s.stride = self.stride
-        s.n_rows = 0 if rows is None else rows.shape[0]
-        s.resid_lambdas, s.x0_lambdas = self.col('resid_lambdas'), self.col('x0_lambdas')
-        s.wte, s.lm_head = self.col('transformer.wte.weight'), self.col('lm_head.weight')
+    def cols(self, n_layer):
+        """The slice columns the population forward reads, as a flat list: resid_lambdas, x0_lambdas, wte, lm_head,
+        then per block c_q, c_k, c_v, c_proj, ve_gate, c_fc, mlp_proj, ve (-1 on blocks without value embeddings)."""
+        out = [self.col('resid_lambdas'), self.col('x0_lambdas'), self.col('transformer.wte.weight'),
+               self.col('lm_head.weight')]
         for i in range(n_layer):
             pre = f'transformer.h.{i}.'
-            s.c_q[i] = self.col(pre + 'attn.c_q.weight')
-            s.c_k[i] = self.col(pre + 'attn.c_k.weight')
-            s.c_v[i] = self.col(pre + 'attn.c_v.weight')
-            s.c_proj[i] = self.col(pre + 'attn.c_proj.weight')
-            s.c_fc[i] = self.col(pre + 'mlp.c_fc.weight')
-            s.mlp_proj[i] = self.col(pre + 'mlp.c_proj.weight')
-            if pre + 'attn.ve_gate.weight' in self.index:
-                s.ve_gate[i] = self.col(pre + 'attn.ve_gate.weight')
-                s.ve[i] = self.col(f'value_embeds.{i}.weight')
-        return s
+            ve = pre + 'attn.ve_gate.weight' in self.index
+            out += [self.col(pre + 'attn.c_q.weight'), self.col(pre + 'attn.c_k.weight'),
+                    self.col(pre + 'attn.c_v.weight'), self.col(pre + 'attn.c_proj.weight'),
+                    self.col(pre + 'attn.ve_gate.weight') if ve else -1, self.col(pre + 'mlp.c_fc.weight'),
+                    self.col(pre + 'mlp.c_proj.weight'), self.col(f'value_embeds.{i}.weight') if ve else -1]
+        return out
+
+    def struct(self, rows, n_layer):
+        return perturbation_struct(rows, self.stride, self.cols(n_layer), n_layer)
+
+
+def perturbation_struct(rows, stride, cols, n_layer):
+    """The noise_perturbation struct: rows fp32 [n_rows, stride] (or None) and the flat column list of
+    NoiseLayout.cols."""
+    s = _lib.NoisePerturbation()
+    s.rows = None if rows is None else rows.data_ptr()
+    s.stride = stride
+    s.n_rows = 0 if rows is None else rows.shape[0]
+    s.resid_lambdas, s.x0_lambdas, s.wte, s.lm_head = cols[:4]
+    for i in range(n_layer):
+        c = cols[4 + 8 * i: 12 + 8 * i]
+        s.c_q[i], s.c_k[i], s.c_v[i], s.c_proj[i], s.c_fc[i], s.mlp_proj[i] = c[0], c[1], c[2], c[3], c[5], c[6]
+        if c[4] >= 0:
+            s.ve_gate[i], s.ve[i] = c[4], c[7]
+    return s
 
 
 _WORKSPACE = {}
@@ -142,7 +163,7 @@ def run_forward(model, tokens, targets, member_seq, noise=None, member_row=None,
     return out
 
 
-def lowrank(x, weight, a, b, sign):
+def _lowrank(x, weight, a, b, sign):
     """x [m, T, in] (or one [T, in] shared by every member, which the reference's broadcasting also takes) through
     W [out, in] + sign a b^T, one (a [m, out], b [m, in], sign [m]) per member (eggroll.py:56-58): fp32 [m, T, out].
     Per-member x: one grouped bf16 MFMA GEMM with the rank-1 term in its epilogue. Shared x: x W^T once per tile,
@@ -198,7 +219,7 @@ def lowrank_sumsq(x, weight, rows, a_off, b_off, sign, mode='expansion'):
     return out
 
 
-def lowrank_embed(weight, a, b, idx, sign):
+def _lowrank_embed(weight, a, b, idx, sign):
     """Embedding rows of W [V, d] + sign a b^T for token ids idx [T] (eggroll.py:61-63): fp32 [m, T, d] on
     noise_lowrank_embed, from a [m, V], b [m, d], sign [m] (W fp32 or bf16)."""
     _lib.require_device(weight, a, b, idx, sign)
@@ -226,22 +247,130 @@ def pack_noise(layout, noise, m, device):
     return torch.cat([p.to(device=device, dtype=torch.float32) for p in parts], 1).contiguous()
 
 
+def kernel_weights(model, params, T):
+    """The device tensors noise_population_forward reads, in the population_forward op's order: resid_lambdas,
+    x0_lambdas and wte (fp32), lm_head (bf16), the rotary cos and sin (fp32 [T, 32]), then per block the stacked
+    c_q|c_k|c_v, attn.c_proj, mlp.c_fc and mlp.c_proj weights (bf16) and, on blocks with value embeddings, ve_gate and
+    the value table (fp32). Plain torch ops on params (name -> tensor), so a compiled caller traces them."""
+    bf = lambda t: t.detach().to(torch.bfloat16).contiguous()
+    f32 = lambda t: t.detach().to(torch.float32).contiguous()
+    cos, sin = model.rope_tables(T)
+    out = [f32(params['resid_lambdas']), f32(params['x0_lambdas']), f32(params['transformer.wte.weight']),
+           bf(params['lm_head.weight']), cos, sin]
+    for i in range(model.config.n_layer):
+        pre = f'transformer.h.{i}.'
+        out += [bf(torch.cat([params[pre + 'attn.c_q.weight'], params[pre + 'attn.c_k.weight'],
+                              params[pre + 'attn.c_v.weight']])),
+                bf(params[pre + 'attn.c_proj.weight']), bf(params[pre + 'mlp.c_fc.weight']),
+                bf(params[pre + 'mlp.c_proj.weight'])]
+        if pre + 'attn.ve_gate.weight' in params:
+            out += [f32(params[pre + 'attn.ve_gate.weight']), f32(params[f'value_embeds.{i}.weight'])]
+    return out
+
+
+@torch.library.custom_op('noise_amd::population_forward', mutates_args=())
+def population_forward_op(weights: list[torch.Tensor], rows: torch.Tensor, tokens: torch.Tensor,
+                          targets: torch.Tensor, member_seq: torch.Tensor, member_row: torch.Tensor,
+                          member_sign: torch.Tensor, n_layer: int, vocab: int, windows: list[int],
+                          ve_layers: list[int], cols: list[int]) -> torch.Tensor:
+    """Per-member summed CE [members] of noise_population_forward: weights as kernel_weights lists them, noise rows
+    fp32 [n_rows, stride], tokens / targets int64 [n_seq, T], the member tables int32 / int32 / fp32 [members],
+    cols as NoiseLayout.cols. The eager body of the op: it builds the ctypes structs from the tensors' pointers."""
+    dev = tokens.device
+    _lib.require_device(rows, tokens, targets, member_seq, member_row, member_sign, *weights)
+    if len(windows) != n_layer or len(ve_layers) != n_layer or len(cols) != 4 + 8 * n_layer or \
+            len(weights) != 6 + 4 * n_layer + 2 * sum(1 for v in ve_layers if v):
+        raise ValueError('population_forward: weights, windows, ve_layers and cols do not match n_layer')
+    if n_layer > _lib.MAX_LAYERS:
+        raise ValueError(f'n_layer {n_layer} > {_lib.MAX_LAYERS}')
+    n_seq, T = tokens.shape
+    members = member_seq.numel()
+    s = _lib.NoiseGpt()
+    s.n_layer, s.vocab, s.padded_vocab = n_layer, vocab, weights[3].shape[0]
+    s.resid_lambdas, s.x0_lambdas, s.wte, s.lm_head, s.rope_cos, s.rope_sin = (w.data_ptr() for w in weights[:6])
+    k = 6
+    for i in range(n_layer):
+        L = s.layers[i]
+        L.w_qkv, L.w_proj, L.w_fc, L.w_mlp_proj = (w.data_ptr() for w in weights[k:k + 4])
+        k += 4
+        if ve_layers[i]:
+            L.w_gate, L.ve = weights[k].data_ptr(), weights[k + 1].data_ptr()
+            k += 2
+        L.window = int(windows[i])
+
+    class _Layout:  # the stride the table checks compare against
+        stride = rows.shape[1]
+    _check_tables(tokens, targets, member_seq, rows, member_row, member_sign, _Layout, dev, False)
+    pert = perturbation_struct(rows, rows.shape[1], cols, n_layer)
+    loss = torch.empty(members, dtype=torch.float32, device=dev)
+    ws = workspace(dev, _lib.lib().noise_population_forward_workspace(members, T))
+    _lib.call('noise_population_forward', ctypes.byref(s), ctypes.byref(pert), _lib.ptr(tokens), _lib.ptr(targets),
+              n_seq, T, _lib.ptr(member_seq), _lib.ptr(member_row), _lib.ptr(member_sign), members, _lib.ptr(loss),
+              None, None, _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+    return loss
+
+
+@population_forward_op.register_fake
+def _(weights, rows, tokens, targets, member_seq, member_row, member_sign, n_layer, vocab, windows, ve_layers, cols):
+    return member_seq.new_empty(member_seq.shape, dtype=torch.float32)
+
+
+@torch.library.custom_op('noise_amd::lowrank', mutates_args=())
+def lowrank_op(x: torch.Tensor, weight: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+               sign: torch.Tensor) -> torch.Tensor:
+    return _lowrank(x, weight, a, b, sign)
+
+
+@lowrank_op.register_fake
+def _(x, weight, a, b, sign):
+    return x.new_empty((sign.numel(), x.shape[-2], weight.shape[0]), dtype=torch.float32)
+
+
+@torch.library.custom_op('noise_amd::lowrank_embed', mutates_args=())
+def lowrank_embed_op(weight: torch.Tensor, a: torch.Tensor, b: torch.Tensor, idx: torch.Tensor,
+                     sign: torch.Tensor) -> torch.Tensor:
+    return _lowrank_embed(weight, a, b, idx, sign)
+
+
+@lowrank_embed_op.register_fake
+def _(weight, a, b, idx, sign):
+    return weight.new_empty((a.shape[0], idx.numel(), weight.shape[1]), dtype=torch.float32)
+
+
+def lowrank(x, weight, a, b, sign):
+    """x [m, T, in] (or one [T, in] shared by every member, which the reference's broadcasting also takes) through
+    W [out, in] + sign a b^T, one (a [m, out], b [m, in], sign [m]) per member (eggroll.py:56-58): fp32 [m, T, out],
+    as the custom op noise_amd::lowrank (so a compiled caller keeps it in its graph)."""
+    return torch.ops.noise_amd.lowrank(x, weight, a, b, sign)
+
+
+def lowrank_embed(weight, a, b, idx, sign):
+    """Embedding rows of W [V, d] + sign a b^T for token ids idx [T] (eggroll.py:61-63): fp32 [m, T, d], as the
+    custom op noise_amd::lowrank_embed."""
+    return torch.ops.noise_amd.lowrank_embed(weight, a, b, idx, sign)
+
+
 def population_loss(model, p, noise, sign, idx, targets):
-    """Mean cross-entropy [m] of m perturbed models on one sequence (eggroll.py:66-103). p is accepted for the
-    reference's signature; the model's own parameters are used. noise: name -> (a [m, out], b [m, in]) or eps [m, L]."""
-    del p
+    """Mean cross-entropy [m] of m perturbed models on one sequence (eggroll.py:66-103), the model's weights taken
+    from p (name -> tensor, the reference's parameters by name; None: the model's own). noise: name -> (a [m, out],
+    b [m, in]) or eps [m, L]. The forward itself is the custom op noise_amd::population_forward, and everything around
+    it is plain torch, so torch.compile(population_loss) (the reference compiles it, eggroll.py:115) traces the whole
+    call into one graph with no break."""
+    params = p if p is not None else dict(model.named_parameters())
     dev = model.lm_head.weight.device
     layout = NoiseLayout(model)
+    n_layer = model.config.n_layer
     m, T = sign.shape[0], idx.shape[0]
     rows = pack_noise(layout, noise, m, dev)
     Tp = (T + 127) // 128 * 128
     tok = torch.nn.functional.pad(idx.to(torch.int64), (0, Tp - T)).view(1, Tp).contiguous()
     tg = torch.nn.functional.pad(targets.to(torch.int64), (0, Tp - T), value=-1).view(1, Tp).contiguous()
-    out = run_forward(model, tok, tg, member_seq=torch.zeros(m, dtype=torch.int32, device=dev), noise=rows,
-                      member_row=torch.arange(m, dtype=torch.int32, device=dev),
-                      member_sign=sign.to(device=dev, dtype=torch.float32).contiguous(), layout=layout,
-                      check_tables=False)
-    return out['loss_sum'] / T
+    ve_layers = [int(f'transformer.h.{i}.attn.ve_gate.weight' in layout.index) for i in range(n_layer)]
+    loss = torch.ops.noise_amd.population_forward(
+        kernel_weights(model, params, Tp), rows, tok, tg, torch.zeros(m, dtype=torch.int32, device=dev),
+        torch.arange(m, dtype=torch.int32, device=dev), sign.to(device=dev, dtype=torch.float32).contiguous(),
+        n_layer, model.config.vocab_size, [int(w) for w, _ in model.window_sizes], ve_layers, layout.cols(n_layer))
+    return loss / T
 
 
 class Eggroll:

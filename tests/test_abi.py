@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_lib.EXPORTS)
-    assert lib.noise_abi_version() == 4 == _lib.ABI_VERSION
+    assert lib.noise_abi_version() == 5 == _lib.ABI_VERSION
 
 
 def test_argument_errors_raise_before_any_gpu_call():
