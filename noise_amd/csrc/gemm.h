@@ -16,6 +16,11 @@
 //
 // MFMA 32x32x16 bf16 lane layout (checked on gfx950): lane l supplies A[row l%32][k 8(l/32)..8(l/32)+7] and
 // B^T[col l%32][same k]; accumulator register r holds C[row (r/4)*8 + (l/32)*4 + r%4][col l%32].
+// Staged epilogues take the transposed product (the weight fragment as the MFMA's A operand, the activation fragment
+// as its B: both operands are "32 rows x 8 k per lane", so the fragments are the same): register r of lane l then
+// holds C[row l%32][col (r/4)*8 + (l/32)*4 + r%4], four consecutive columns of one row per register quad, and the
+// tile is staged with one 8-byte LDS write per quad (32 per wave of 64 x 128) instead of a 2-byte write per value
+// (128). The sums are the same products in the same order: the outputs are bit-identical either way.
 #pragma once
 
 #include <type_traits>
@@ -41,7 +46,7 @@ struct GemmShape {
   static constexpr int kADma = BM / 16 / kWaves, kBDma = BN / 16 / kWaves;  // 1 KB direct-to-LDS loads per wave
                                                                           // and step
   static constexpr int kDma = kADma + kBDma;
-  static constexpr int kEpiLd = BN + 16;                  // bf16 staging row stride (16 elements of padding)
+  static constexpr int kEpiLd = BN + 4;                   // bf16 staging row stride (4 elements of padding)
   static constexpr int kMainLds = kStages * kStageBytes;
   static constexpr int kEpiLds = BM * kEpiLd * 2;         // the whole tile in bf16
   static constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
@@ -55,6 +60,15 @@ struct GemmShape {
   static_assert(kStages >= 2 && kStages <= 4, "stages");
   static_assert(kLdsBytes * kMinBlocks <= 160 * 1024, "LDS");
 };
+
+// One 32 x 32 x 16 product of an activation fragment a and a weight fragment b into c: C = A B^T, or with kT its
+// transpose (b as the MFMA's A operand), whose accumulator holds four consecutive columns of one row per register
+// quad.
+template <bool kT>
+__device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return kT ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0)
+            : __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -227,8 +241,10 @@ template <class S, class Epi>
 __device__ __forceinline__ void staged_epilogue(const Epi& epi, f32x16 (&acc)[S::TM][S::TN], unsigned char* smem_raw,
                                                 int M, int m0, int n0, int n_tile, int wave, int wm, int wn,
                                                 int lane) {
-  // The accumulators are rounded to bf16 -- the rounding of the reference's bf16 autocast matmul output, to which it
-  // then adds its fp32 rank-1 term -- and staged as the whole tile. Each wave then takes
+  // The accumulators (transposed: four consecutive columns of one row per register quad) are rounded to bf16 -- the
+  // rounding of the reference's bf16 autocast matmul output, to which it then adds its fp32 rank-1 term -- and staged
+  // as the whole tile, 8 bytes per write; the row pitch BN + 4 puts the 32 rows of one write on distinct pairs of the
+  // 64 banks (the pitch is 2 mod 64 words). Each wave then takes
   // kWaveRows rows (one member's: M and the member length are multiples of 64) in groups of Epi::kRows (8, or 4 for
   // epilogues that prefetch much per row); lane l holds
   // columns 4l .. 4l+3 of each 256-column half. The epilogue functor provides
@@ -255,9 +271,11 @@ __device__ __forceinline__ void staged_epilogue(const Epi& epi, f32x16 (&acc)[S:
 #pragma unroll
     for (int j = 0; j < S::TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lr = wm * S::WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        st[lr * S::kEpiLd + wn * S::WTN + j * 32 + (lane & 31)] = f32_to_bf16(acc[i][j][r]);
+      for (int q = 0; q < 4; ++q) {
+        const int lr = wm * S::WTM + i * 32 + (lane & 31);
+        const int lc = wn * S::WTN + j * 32 + q * 8 + (lane >> 5) * 4;
+        *(u32x2*)(st + lr * S::kEpiLd + lc) = u32x2{pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                                    pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
       }
   __syncthreads();
   if (row_base >= M) return;
@@ -354,6 +372,7 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   constexpr int kTileStride = 32 * S::BK * 2;  // bytes between the 32-row MFMA tiles of a stage
 
   f32x16 acc[S::TM][S::TN];  // first written by step 0's first MFMAs, which take a zero accumulator
+  constexpr bool kTr = !AccEpilogue<Epi>::value;  // staged epilogues take the transposed tile
 
   // Prologue: steps 0 .. NS - 1 in flight; stage 0 visible; its first k-substep's fragments read.
 #pragma unroll
@@ -383,8 +402,7 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
     for (int i = 0; i < S::TM; ++i)
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0a[i], f0b[j], decltype(first)::value ? f32x16{} : acc[i][j],
-                                                            0, 0, 0);
+        acc[i][j] = mma<kTr>(f0a[i], f0b[j], decltype(first)::value ? f32x16{} : acc[i][j]);
     first_half_schedule<S>();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -401,7 +419,7 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
     for (int i = 0; i < S::TM; ++i)
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1a[i], f1b[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = mma<kTr>(f1a[i], f1b[j], acc[i][j]);
     second_half_schedule<S>();
     __builtin_amdgcn_sched_barrier(0);
   };

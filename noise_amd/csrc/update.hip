@@ -56,8 +56,9 @@ __global__ __launch_bounds__(1024) void fitness_kernel(const float* __restrict__
 // as rows [pair][128] padded to 160 floats, so the two pair rows of one operand read (lanes 0..31 and 32..63) fall
 // in opposite halves of the 64 banks. Every load is a 256-byte row segment (thread: one column, 8 of the 16 rows);
 // columns past out / in and pairs past the last read as zeros, so offsets and sizes need no alignment.
-// One launch covers a list of matrices (jobs, by value in the kernel arguments): workgroup b takes tile b - tile0 of
-// the job whose tile range holds b, tiles in row-major order over ceil(out / 128) x ceil(in / 128).
+// One launch covers a list of matrices (jobs, by value in the kernel arguments): the launch's tiles are numbered job by
+// job, each job's in row-major order over ceil(out / 128) x ceil(in / 128); tile t belongs to the job whose range
+// [tile0, next tile0) holds it, and each XCD takes a contiguous run of tile numbers.
 constexpr int kOgTile = 128, kOgK = 16, kOgPitch = 160, kOgMaxJobs = 64;
 
 struct OgJob {
@@ -69,6 +70,7 @@ struct OgJob {
 struct OgJobs {
   int32_t n;
   int32_t accumulate;  // add to the gradients instead of overwriting them
+  int32_t total;       // tiles of the launch (the grid is that rounded up to a multiple of 8)
   OgJob job[kOgMaxJobs];
 };
 
@@ -80,12 +82,17 @@ __global__ __launch_bounds__(256) void outer_grad_kernel(const float* __restrict
                                                          OgJobs jobs) {
   __shared__ float as[2][kOgK][kOgPitch];
   __shared__ float bs[2][kOgK][kOgPitch];
+  // Workgroups are dispatched round-robin over the 8 XCDs; XCD x takes the contiguous tile range
+  // [x per, (x + 1) per), so the tiles of one matrix, which read the same a and b slices, share one L2.
+  const int per = (int)(gridDim.x / 8);
+  const int tid_ = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (tid_ >= jobs.total) return;  // the grid's round-up
   int jb = 0;
-  while (jb + 1 < jobs.n && (int)blockIdx.x >= jobs.job[jb + 1].tile0) ++jb;
+  while (jb + 1 < jobs.n && tid_ >= jobs.job[jb + 1].tile0) ++jb;
   const OgJob& job = jobs.job[jb];
   const int64_t a_off = job.a_off, b_off = job.b_off, out = job.out, in = job.in;
   float* __restrict__ grad = job.grad;
-  const int tile = (int)blockIdx.x - job.tile0;
+  const int tile = tid_ - job.tile0;
   const int64_t o0 = (int64_t)(tile / job.n_in_tiles) * kOgTile, i0 = (int64_t)(tile % job.n_in_tiles) * kOgTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wo = (wave >> 1) * 64, wi = (wave & 1) * 64;
@@ -335,8 +342,10 @@ extern "C" int noise_outer_grad_batch(const float* rows, int64_t stride, const f
       NOISE_REQUIRE(tiles <= INT32_MAX, "too many tiles");
     }
     if (tiles == 0) continue;
-    hipLaunchKernelGGL(outer_grad_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, rows, stride,
-                       (const void*)rows, stride, 0, weight, pairs, scale, jobs);
+    NOISE_REQUIRE(tiles + 7 <= INT32_MAX, "too many tiles");
+    jobs.total = (int32_t)tiles;
+    hipLaunchKernelGGL(outer_grad_kernel, dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256), 0, (hipStream_t)stream,
+                       rows, stride, (const void*)rows, stride, 0, weight, pairs, scale, jobs);
     NOISE_LAUNCH_CHECK();
   }
   return NOISE_OK;
@@ -356,10 +365,11 @@ extern "C" int noise_reassemble(const float* error, int64_t error_ld, const void
   g.out = (int32_t)d_out; g.in = (int32_t)d_in; g.grad = grad;
   g.n_in_tiles = (int32_t)((d_in + kOgTile - 1) / kOgTile);
   const int64_t tiles = (int64_t)g.n_in_tiles * ((d_out + kOgTile - 1) / kOgTile);
-  NOISE_REQUIRE(tiles <= INT32_MAX, "too many tiles");
+  NOISE_REQUIRE(tiles + 7 <= INT32_MAX, "too many tiles");
+  jobs.total = (int32_t)tiles;
   NoiseTimer tm(kTimeReassemble, (hipStream_t)stream);
-  hipLaunchKernelGGL(outer_grad_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, error, error_ld, x,
-                     x_ld, x_bf16 ? 1 : 0, (const float*)nullptr, tokens, scale, jobs);
+  hipLaunchKernelGGL(outer_grad_kernel, dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(256), 0, (hipStream_t)stream,
+                     error, error_ld, x, x_ld, x_bf16 ? 1 : 0, (const float*)nullptr, tokens, scale, jobs);
   NOISE_LAUNCH_CHECK();
   return NOISE_OK;
 }
