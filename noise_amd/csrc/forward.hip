@@ -15,6 +15,11 @@ namespace noise {
 
 constexpr float kNormEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps, F.rms_norm's default
 
+// The lambda mix l_r x + l_0 x0 (eggroll.py:77-79), spelled as one multiply and one fma so that every kernel that forms
+// it (the embedding kernel for block 0's input, the projections that recompute that input or mix the next block's)
+// rounds it the same way.
+__device__ __forceinline__ float lambda_mix(float lr, float l0, float x, float x0) { return fmaf(l0, x0, lr * x); }
+
 // The member tables. A member whose token row is outside [0, n_seq) or whose noise row is outside [0, n_rows) reads
 // row 0 of both (so every access stays inside its buffer) and is marked bad: the embedding gives its rows NaN and the
 // CE finalization writes NaN for every one of its tokens, so its loss is NaN (the reference's indexing would raise).
@@ -74,6 +79,7 @@ struct EmbedMix {
   const float* x0_lambdas;
   int64_t off_resid, off_x0, off_b[3];
   int write_x0;
+  int write_x;  // 0: block 0's attn c_proj rebuilds x from x0 itself
 };
 
 __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __restrict__ wte, int Vp, int64_t off_wte,
@@ -141,14 +147,16 @@ __global__ __launch_bounds__(256) void embed_kernel(Members mb, const float* __r
   }
   {
     float lr = em.resid_lambdas[0], l0 = em.x0_lambdas[0];
-    if (nr) { lr += s * nr[em.off_resid]; l0 += s * nr[em.off_x0]; }
+    if (nr) { lr = fmaf(s, nr[em.off_resid], lr); l0 = fmaf(s, nr[em.off_x0], l0); }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) e[q][j] = lr * e[q][j] + l0 * e[q][j];  // x
-      float* dst = em.x + (r0 + q) * kD + c0;
-      *(f32x4*)dst = f32x4{e[q][0], e[q][1], e[q][2], e[q][3]};
-      *(f32x4*)(dst + 4) = f32x4{e[q][4], e[q][5], e[q][6], e[q][7]};
+      for (int j = 0; j < 8; ++j) e[q][j] = lambda_mix(lr, l0, e[q][j], e[q][j]);  // x
+      if (em.write_x) {  // otherwise block 0's attn c_proj rebuilds x from x0 (EpiResidNorm kXBase)
+        float* dst = em.x + (r0 + q) * kD + c0;
+        *(f32x4*)dst = f32x4{e[q][0], e[q][1], e[q][2], e[q][3]};
+        *(f32x4*)(dst + 4) = f32x4{e[q][4], e[q][5], e[q][6], e[q][7]};
+      }
       ss[q] = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss[q] += e[q][j] * e[q][j];
@@ -219,10 +227,13 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(Members mb, NormArgs a) {
   for (int j = 0; j < 4; ++j) { v[j] = v0[j]; v[j + 4] = v1[j]; }
   if (a.mix) {
     float lr = a.resid_lambdas[a.layer], l0 = a.x0_lambdas[a.layer];
-    if (nr) { lr += s * nr[a.off_resid + a.layer]; l0 += s * nr[a.off_x0 + a.layer]; }
+    if (nr) { lr = fmaf(s, nr[a.off_resid + a.layer], lr); l0 = fmaf(s, nr[a.off_x0 + a.layer], l0); }
     const f32x4 w0 = *(const f32x4*)(a.x0 + r * kD + c0), w1 = *(const f32x4*)(a.x0 + r * kD + c0 + 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) { v[j] = lr * v[j] + l0 * w0[j]; v[j + 4] = lr * v[j + 4] + l0 * w1[j]; }
+    for (int j = 0; j < 4; ++j) {
+      v[j] = lambda_mix(lr, l0, v[j], w0[j]);
+      v[j + 4] = lambda_mix(lr, l0, v[j + 4], w1[j]);
+    }
     float* dst = a.x + r * kD + c0;
     *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
     *(f32x4*)(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
@@ -457,8 +468,12 @@ struct EpiQKV {
 // 4 rows keep the x and x0 prefetch small. The rank-1 term is added unconditionally: its a and dot are zero for rows
 // without noise. x and h are written with non-temporal stores: neither is read again before it has left the caches.
 // kFinal: the last block's c_proj, after which x is not read again: only h and the dots are stored.
-template <bool kMix, int kNDot, bool kJit = false, bool kX0 = false, bool kFinal = false>
+// kXBase: block 0's attn c_proj when the embedding kernel stored no x: the residual it adds to is block 0's input
+// x = (l_r + s eps_r) x0 + (l_0 + s eps_0) x0, rebuilt from the recomputed x0 (kX0) with embed_kernel's operations, so
+// it is bit-identical to the x the embedding kernel would have stored, and 2 KB per row are neither written nor read.
+template <bool kMix, int kNDot, bool kJit = false, bool kX0 = false, bool kFinal = false, bool kXBase = false>
 struct EpiResidNorm {
+  static_assert(!kXBase || (kX0 && !kMix), "block 0's input comes from the recomputed x0, with no mix after it");
   static constexpr int kRows = 4;
   Members mb;
   float* x;             // [M, 512] residual stream, read and written
@@ -474,7 +489,7 @@ struct EpiResidNorm {
   int64_t off_wte;
   const float* resid_lambdas;
   const float* x0_lambdas;
-  int layer;            // the block whose lambdas mix
+  int layer;            // the block whose lambdas mix (kXBase: block 0, whose lambdas form its input)
   int64_t off_resid, off_x0;
   bf16_t* h;            // [M, 512]
   int64_t off_b[3];     // noise offsets of the next linear's b vectors (kNDot of them)
@@ -542,10 +557,10 @@ struct EpiResidNorm {
       }
     }
     w.lr = 1.f; w.l0 = 0.f;
-    if (kMix) {
+    if (kMix || kXBase) {
       w.lr = resid_lambdas[layer];
       w.l0 = x0_lambdas[layer];
-      if (w.nr) { w.lr += w.s * w.nr[off_resid + layer]; w.l0 += w.s * w.nr[off_x0 + layer]; }
+      if (w.nr) { w.lr = fmaf(w.s, w.nr[off_resid + layer], w.lr); w.l0 = fmaf(w.s, w.nr[off_x0 + layer], w.l0); }
     }
   }
   __device__ __forceinline__ void ready(Wave& w) const {
@@ -558,7 +573,7 @@ struct EpiResidNorm {
       const int tq = kX0 ? lane_val(w.tok, row0 - w.row_base + q) : 0;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        p.xv[q][hh] = ld4(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
+        if (!kXBase) p.xv[q][hh] = ld4(x + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
         if (kX0) p.x0v[q][hh] = ld4(wte + (int64_t)tq * kD + hh * 256 + 4 * lane);  // the embedding row
         else if (kMix) p.x0v[q][hh] = ld4(x0 + (int64_t)(row0 + q) * kD + hh * 256 + 4 * lane);
       }
@@ -583,14 +598,15 @@ struct EpiResidNorm {
       ss[q] = 0.f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        f32x4 xn = p.xv[q][hh];
+        f32x4 xn = kXBase ? f32x4{0.f, 0.f, 0.f, 0.f} : p.xv[q][hh];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float val = v[q][hh][e];
           val += w.s * d * w.a[hh][e];
-          xn[e] += val;
           const float x0e = kX0 ? fmaf(at, w.bw[hh][e], p.x0v[q][hh][e]) * inv : p.x0v[q][hh][e];
-          if (kMix) xn[e] = w.lr * xn[e] + w.l0 * x0e;
+          if (kXBase) xn[e] = lambda_mix(w.lr, w.l0, x0e, x0e);  // block 0's input, as embed_kernel forms it
+          xn[e] += val;
+          if (kMix) xn[e] = lambda_mix(w.lr, w.l0, xn[e], x0e);
           ss[q] += xn[e] * xn[e];
         }
         v[q][hh] = xn;
@@ -938,6 +954,7 @@ static int prepare_all() {
   NOISE_CHECK_HIP((prepare_gemm<RowTile, EpiResidNorm<true, 3, false, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<ProjTile, EpiResidNorm<false, 1>>()));
   NOISE_CHECK_HIP((prepare_gemm<ProjTile, EpiResidNorm<false, 1, true>>()));
+  NOISE_CHECK_HIP((prepare_gemm<ProjTile, EpiResidNorm<false, 1, false, true, false, true>>()));
   NOISE_CHECK_HIP((prepare_gemm<Tile, EpiHeadCE>()));
   g_prepared = true;
   return NOISE_OK;
@@ -1022,6 +1039,9 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
   const int first_layer = from_block ? dr->entry : 0;
   // the λ mix recomputes x0 from the embedding table when this call's embed_kernel formed it without jitter
   const bool x0_recompute = !from_block && !dr->jit(-1, 0).on();
+  // and block 0's attn c_proj rebuilds block 0's input from x0 too, so the embedding kernel stores no x (a capture
+  // keeps the stored x: it copies every block's input)
+  const bool x_from_x0 = x0_recompute && !dr->capture;
 
   hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((T * 16 + 255) / 256)), dim3(256), 0, stream, model->rope_cos,
                      model->rope_sin, T, ws.rope);
@@ -1040,6 +1060,7 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
     em.off_resid = pert->resid_lambdas; em.off_x0 = pert->x0_lambdas;
     em.off_b[0] = pert->c_q[0] + kD; em.off_b[1] = pert->c_k[0] + kD; em.off_b[2] = pert->c_v[0] + kD;
     em.write_x0 = dr->capture != nullptr || !x0_recompute;
+    em.write_x = !x_from_x0;
     hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), 0, stream, mb, model->wte, Vp, pert->wte,
                        dr->jit(-1, 0), ws.x0, ws.x0_inv, em, M);
     NOISE_LAUNCH_CHECK();
@@ -1121,6 +1142,13 @@ static int forward_impl(const noise_gpt* model, const noise_perturbation* pert, 
         memcpy((void*)&ej, (const void*)&ep, sizeof(ep));
         ej.jit = jp;
         NOISE_CHECK_HIP((launch_gemm<ProjTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ej, stream)));
+      } else if (i == 0 && x_from_x0) {
+        EpiResidNorm<false, 1, false, true, false, true> eb;
+        memcpy((void*)&eb, (const void*)&ep, sizeof(ep));
+        eb.wte = model->wte; eb.x0_inv = ws.x0_inv; eb.Vp = Vp; eb.off_wte = pert->wte;
+        eb.resid_lambdas = model->resid_lambdas; eb.x0_lambdas = model->x0_lambdas; eb.layer = 0;
+        eb.off_resid = pert->resid_lambdas; eb.off_x0 = pert->x0_lambdas;
+        NOISE_CHECK_HIP((launch_gemm<ProjTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, eb, stream)));
       } else {
         NOISE_CHECK_HIP((launch_gemm<ProjTile>(ws.y, kD, L.w_proj, kD, (int)M, kD, kD, ep, stream)));
       }
