@@ -6,12 +6,15 @@
 // v_mfma_f32_32x32x16_bf16), or one of the tiles with waves of 64 x 128: 128 x 512 with 2 x 4 waves and 64 x 512
 // with 1 x 4 waves (whole 512-wide rows, for epilogues that normalize rows), 128 x 256 with 2 x 2 waves. The
 // 128 x 256 and 64 x 512 tiles are sized for two workgroups per CU, so that one workgroup's epilogue runs beside
-// the other's MFMAs. K advances in steps of 32 through kStages LDS stages filled by direct-to-LDS buffer loads
-// (buffer_load_dwordx4 ... lds): the loads of step kt + kStages are issued as soon as every wave is done with step
-// kt, so kStages - 1 steps of loads are in flight behind the MFMAs and no register holds staged data.
-// One barrier per step, placed between the step's two 16-deep k-substeps: the second k-substep's fragments are
-// read before it and the next step's first fragments after it, so LDS latency hides behind MFMAs.
-// An LDS row is 32 bf16 = 4 16-byte chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 lanes of a
+// the other's MFMAs. K advances in steps of 32 or 64 (BK) through kStages LDS stages filled by direct-to-LDS buffer
+// loads (buffer_load_dwordx4 ... lds): the loads of step kt + kStages are issued as soon as every wave is done with
+// step kt, so kStages - 1 steps of loads are in flight behind the MFMAs and no register holds staged data.
+// One barrier per step, placed before the step's last 16-deep k-substep: the last k-substep's fragments are read
+// before it and the next step's first fragments after it, so LDS latency hides behind MFMAs. 64-deep steps in two
+// stages halve the barriers and waits per K against 32-deep steps in four (the same LDS): on random bf16 operands at
+// M = 2^20 the 128 x 512 tile (N = 512, K = 2048) went from 929 to 1041 TFLOP/s and the 8-wave 256 x 256 tile from
+// 828 to 867 (N = 2048, K = 512), with bit-identical outputs.
+// An LDS row is BK bf16 = 4 or 8 16-byte chunks, swizzled by row (lds_swizzle) so that the 16 lanes of a
 // ds_read_b128 phase (16 consecutive rows, one chunk) touch 16 distinct bank groups.
 //
 // MFMA 32x32x16 bf16 lane layout (checked on gfx950): lane l supplies A[row l%32][k 8(l/32)..8(l/32)+7] and
@@ -43,21 +46,25 @@ struct GemmShape {
   static constexpr int kStages = NS_;                 // LDS stages
   static constexpr int kMinBlocks = MINB_;            // workgroups per CU the registers and LDS are sized for
   static constexpr int kStageBytes = (BM + BN) * BK * 2;  // A rows then B rows
-  static constexpr int kADma = BM / 16 / kWaves, kBDma = BN / 16 / kWaves;  // 1 KB direct-to-LDS loads per wave
-                                                                          // and step
+  static constexpr int kRowBytes = BK * 2;                // one LDS row: 4 (BK 32) or 8 (BK 64) 16-byte chunks
+  static constexpr int kLoadRows = 1024 / kRowBytes;      // rows per 1 KB direct-to-LDS load
+  static constexpr int kSub = BK / 16;                    // 16-deep k-substeps per step
+  static constexpr int kADma = BM / kLoadRows / kWaves, kBDma = BN / kLoadRows / kWaves;  // loads per wave and step
   static constexpr int kDma = kADma + kBDma;
   static constexpr int kEpiLd = BN + 4;                   // bf16 staging row stride (4 elements of padding)
   static constexpr int kMainLds = kStages * kStageBytes;
   static constexpr int kEpiLds = BM * kEpiLd * 2;         // the whole tile in bf16
   static constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
   static constexpr int kWaveRows = BM / kWaves;           // epilogue rows per wave
-  static_assert(BK == 32 && WTN == 128 && (WTM == 128 || WTM == 64) && (kWaves == 4 || kWaves == 8),
-                "main loop: 4 or 8 waves of 128x128 or 64x128, K steps of 32");
-  static_assert(kADma * kWaves * 16 == BM && kBDma * kWaves * 16 == BN, "row groups of 16 split evenly over waves");
+  static_assert((BK == 32 || BK == 64) && WTN == 128 && (WTM == 128 || WTM == 64) && (kWaves == 4 || kWaves == 8),
+                "main loop: 4 or 8 waves of 128x128 or 64x128, K steps of 32 or 64");
+  static_assert(kADma * kWaves * kLoadRows == BM && kBDma * kWaves * kLoadRows == BN,
+                "row groups of one load split evenly over waves");
   static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 512) || (BM == 128 && BN == 256) ||
                     (BM == 64 && BN == 512),
                 "tiles: 256x256, 128x512, 128x256 or 64x512");
   static_assert(kStages >= 2 && kStages <= 4, "stages");
+  static_assert((kStages - 1) * kDma < 64, "loads in flight: the vmcnt field");
   static_assert(kLdsBytes * kMinBlocks <= 160 * 1024, "LDS");
 };
 
@@ -71,6 +78,15 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// The 16-byte chunk slot of LDS row r: chunk c of the row sits in slot c ^ lds_swizzle<BK>(r). With 64-byte rows
+// (BK 32) a ds_read_b128 phase of 16 consecutive rows and one chunk covers rows r .. r + 15, four to a 256-byte bank
+// line; (r >> 2) & 3 gives each of the four its own slot. With 128-byte rows (BK 64) two rows share a bank line, and
+// (r >> 1) & 7 gives each of the 8 pairs its own slot. Either way the 16 reads hit 16 distinct groups of 4 banks.
+template <int BK>
+__device__ __forceinline__ int lds_swizzle(int r) {
+  return BK == 32 ? (r >> 2) & 3 : (r >> 1) & 7;
+}
 
 // One 16-byte-per-lane direct-to-LDS buffer load (buffer_load_dwordx4 ... lds): lane l's 16 bytes land at
 // lds + 16 l. The builtin is a gfx950 target builtin, so it is only spelled out in the device pass (the host pass
@@ -180,6 +196,22 @@ __device__ __forceinline__ void second_half_schedule() {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+  } else if constexpr (S::BK == 64) {  // 8 MFMAs, 8 or 10 loads, 6 reads
+    constexpr int kPairs = S::kDma - 6;  // MFMAs followed by two loads; the rest take one
+    static_assert(kPairs >= 0 && kPairs <= 6, "64-deep steps: 6 to 12 loads");
+#pragma unroll
+    for (int g = 0; g < kPairs; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int g = kPairs; g < 6; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   } else if constexpr (S::kDma == 5) {  // 8 MFMAs, 5 loads, 6 reads
 #pragma unroll
     for (int g = 0; g < 5; ++g) {
@@ -334,15 +366,21 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   const __amdgpu_buffer_rsrc_t b_rsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)(B + (int64_t)n0 * ldb), 0, b_rows * (int)ldb * 2, 0x00020000);
 
-  // One direct-to-LDS load fills 1 KB = 16 rows x 4 chunks: lane l writes LDS bytes 16 l .. 16 l + 15, i.e. row
-  // l >> 2, slot l & 3, so it fetches global chunk (l & 3) ^ ((l >> 4) & 3). Wave w fills row groups
-  // w kADma .. (w + 1) kADma - 1 of A and w kBDma .. (w + 1) kBDma - 1 of B.
-  const int drow = lane >> 2, dchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  // One direct-to-LDS load fills 1 KB = kLoadRows rows of kRowBytes: lane l writes LDS bytes 16 l .. 16 l + 15,
+  // i.e. row l / (chunks per row), slot l % (chunks per row), so it fetches the global chunk that the row's swizzle
+  // puts in that slot. Wave w fills row groups w kADma .. (w + 1) kADma - 1 of A and w kBDma .. (w + 1) kBDma - 1
+  // of B.
+  constexpr int kChunks = S::kRowBytes / 16;
+  const int drow = lane / kChunks, dslot = lane % kChunks;
+  auto load_off = [&](int g, int ld) {
+    const int r = g * S::kLoadRows + drow;
+    return (r * ld + (dslot ^ lds_swizzle<S::BK>(r)) * 8) * 2;
+  };
   int a_vo[S::kADma], b_vo[S::kBDma];
 #pragma unroll
-  for (int j = 0; j < S::kADma; ++j) a_vo[j] = (((wave * S::kADma + j) * 16 + drow) * (int)lda + dchunk * 8) * 2;
+  for (int j = 0; j < S::kADma; ++j) a_vo[j] = load_off(wave * S::kADma + j, (int)lda);
 #pragma unroll
-  for (int j = 0; j < S::kBDma; ++j) b_vo[j] = (((wave * S::kBDma + j) * 16 + drow) * (int)ldb + dchunk * 8) * 2;
+  for (int j = 0; j < S::kBDma; ++j) b_vo[j] = load_off(wave * S::kBDma + j, (int)ldb);
   const int nk = K / S::BK;
   // Steps past the last one are issued too, with an offset past the buffer's end: the hardware returns zeros
   // without a memory access, and every step has the same number of loads in flight.
@@ -359,17 +397,18 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
       dma16(b_rsrc, b_base + j * 1024, b_vo[j] + oob, koff);
   };
 
-  // Fragment offsets: row (lane & 31) of a 32-row tile, chunk 2 kk + (lane >> 5), in slot chunk ^ row bits 2..3.
-  const int xs = ((lane & 31) >> 2) & 3;
-  int fa_off[2], fb_off[2];
+  // Fragment offsets of k-substep kk: row (lane & 31) of a 32-row tile, chunk 2 kk + (lane >> 5), in its swizzled
+  // slot (the swizzle repeats every 16 rows, so it holds for every 32-row tile of the stage).
+  const int xs = lds_swizzle<S::BK>(lane & 31);
+  int fa_off[S::kSub], fb_off[S::kSub];
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
+  for (int kk = 0; kk < S::kSub; ++kk) {
     const int ch = ((2 * kk + (lane >> 5)) ^ xs) * 16;
-    fa_off[kk] = (wm * S::WTM + (lane & 31)) * S::BK * 2 + ch;
-    fb_off[kk] = kAStage + (wn * S::WTN + (lane & 31)) * S::BK * 2 + ch;
+    fa_off[kk] = (wm * S::WTM + (lane & 31)) * S::kRowBytes + ch;
+    fb_off[kk] = kAStage + (wn * S::WTN + (lane & 31)) * S::kRowBytes + ch;
   }
   auto frag = [&](int off) { return *(const bf16x8*)(smem_raw + off); };
-  constexpr int kTileStride = 32 * S::BK * 2;  // bytes between the 32-row MFMA tiles of a stage
+  constexpr int kTileStride = 32 * S::kRowBytes;  // bytes between the 32-row MFMA tiles of a stage
 
   f32x16 acc[S::TM][S::TN];  // first written by step 0's first MFMAs, which take a zero accumulator
   constexpr bool kTr = !AccEpilogue<Epi>::value;  // staged epilogues take the transposed tile
@@ -379,47 +418,53 @@ __global__ __launch_bounds__(S::kThreads, S::kMinBlocks) void gemm_nt_kernel(con
   for (int s = 0; s < NS; ++s) dma(s, s);
   wait_vmcnt_imm<(NS - 1) * S::kDma>();
   lds_barrier();
-  bf16x8 f0a[S::TM], f0b[S::TN], f1a[S::TM], f1b[S::TN];
+  bf16x8 fa[2][S::TM], fb[2][S::TN];  // fragments of alternate k-substeps
 #pragma unroll
-  for (int i = 0; i < S::TM; ++i) f0a[i] = frag(fa_off[0] + i * kTileStride);
+  for (int i = 0; i < S::TM; ++i) fa[0][i] = frag(fa_off[0] + i * kTileStride);
 #pragma unroll
-  for (int j = 0; j < S::TN; ++j) f0b[j] = frag(fb_off[0] + j * kTileStride);
+  for (int j = 0; j < S::TN; ++j) fb[0][j] = frag(fb_off[0] + j * kTileStride);
 
-  // Step kt on stage kt % NS: read k-substep 1 and multiply k-substep 0; wait for this wave's reads and for stage
-  // kt + 1's loads, barrier (everyone is then past its reads of stage kt, and stage kt + 1 is visible); refill stage
-  // kt % NS with step kt + NS; read the next step's k-substep 0 and multiply k-substep 1.
-  // The reads and loads of each half are spread between its MFMAs (one per MFMA), so that neither the LDS nor the
+  // Step kt on stage kt % NS: for each k-substep but the last, read the next k-substep and multiply this one; wait
+  // for this wave's reads and for stage kt + 1's loads, barrier (everyone is then past its reads of stage kt, and
+  // stage kt + 1 is visible); refill stage kt % NS with step kt + NS; read the next step's k-substep 0 and multiply
+  // the last k-substep.
+  // The reads and loads of each part are spread between its MFMAs (one per MFMA), so that neither the LDS nor the
   // texture-address queue sees a burst.
   // Step 0 is peeled: its first MFMAs take the inline constant 0 as the accumulator, so the accumulators need no
   // zeroing moves.
   auto step = [&](int kt, auto first) {
     const int pb = (kt % NS) * kStage;
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i) f1a[i] = frag(fa_off[1] + pb + i * kTileStride);
+    for (int kk = 0; kk + 1 < S::kSub; ++kk) {
+      const int nx = (kk + 1) & 1, cu = kk & 1;
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) f1b[j] = frag(fb_off[1] + pb + j * kTileStride);
+      for (int i = 0; i < S::TM; ++i) fa[nx][i] = frag(fa_off[kk + 1] + pb + i * kTileStride);
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i)
+      for (int j = 0; j < S::TN; ++j) fb[nx][j] = frag(fb_off[kk + 1] + pb + j * kTileStride);
 #pragma unroll
-      for (int j = 0; j < S::TN; ++j)
-        acc[i][j] = mma<kTr>(f0a[i], f0b[j], decltype(first)::value ? f32x16{} : acc[i][j]);
-    first_half_schedule<S>();
-    __builtin_amdgcn_sched_barrier(0);
+      for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < S::TN; ++j)
+          acc[i][j] = mma<kTr>(fa[cu][i], fb[cu][j], decltype(first)::value && kk == 0 ? f32x16{} : acc[i][j]);
+      first_half_schedule<S>();
+      __builtin_amdgcn_sched_barrier(0);
+    }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     wait_vmcnt_imm<(NS - 2) * S::kDma>();  // stage kt + 1 has landed (the loads of kt + 2, kt + 3 may still fly)
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     dma(kt + NS, kt % NS);
     const int nb = ((kt + 1) % NS) * kStage;
+    constexpr int kLast = (S::kSub - 1) & 1;  // the last k-substep's fragment set; the next step's first goes in 0
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i) f0a[i] = frag(fa_off[0] + nb + i * kTileStride);
+    for (int i = 0; i < S::TM; ++i) fa[0][i] = frag(fa_off[0] + nb + i * kTileStride);
 #pragma unroll
-    for (int j = 0; j < S::TN; ++j) f0b[j] = frag(fb_off[0] + nb + j * kTileStride);
+    for (int j = 0; j < S::TN; ++j) fb[0][j] = frag(fb_off[0] + nb + j * kTileStride);
 #pragma unroll
     for (int i = 0; i < S::TM; ++i)
 #pragma unroll
       for (int j = 0; j < S::TN; ++j)
-        acc[i][j] = mma<kTr>(f1a[i], f1b[j], acc[i][j]);
+        acc[i][j] = mma<kTr>(fa[kLast][i], fb[kLast][j], acc[i][j]);
     second_half_schedule<S>();
     __builtin_amdgcn_sched_barrier(0);
   };
