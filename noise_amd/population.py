@@ -425,6 +425,16 @@ class Eggroll:
         start = g - g % (2 * self.chunk)
         return members, (g // 2) % self.pairs, torch.where(g % 2 == 0, 1.0, -1.0), start // per_seq
 
+    def gather(self, losses):
+        """Every rank's per-member losses in rank order, which is the whole population's member order (rank r
+        evaluates the r-th contiguous share of it): one all_gather over the default process group
+        (eggroll.py:147-150). On one process, `losses` itself."""
+        if self.world == 1:
+            return losses
+        gathered = [torch.empty_like(losses) for _ in range(self.world)]
+        torch.distributed.all_gather(gathered, losses)
+        return torch.cat(gathered)
+
     # pairs per chunk of the update: each chunk's noise rows are generated, consumed and dropped
     UPDATE_PAIRS = 1024
 
@@ -455,10 +465,7 @@ class Eggroll:
                               noise=rows, member_row=local, member_sign=(sgn[sl] * self.sigma).float().contiguous(),
                               layout=self.layout, check_tables=False)
             losses[sl] = out['loss_sum'] / T
-        if self.world > 1:
-            gathered = [torch.empty_like(losses) for _ in range(self.world)]
-            torch.distributed.all_gather(gathered, losses)
-            losses = torch.cat(gathered)
+        losses = self.gather(losses)
         n_fit = losses.numel() // 2
         fitness = torch.empty(n_fit, dtype=torch.float32, device=self.device)
         weight = torch.empty(self.pairs, dtype=torch.float32, device=self.device)
