@@ -83,6 +83,23 @@ def test_capture_matches_oracle(dev):
     assert ((d.x0.cpu() - st['x0']).norm() / st['x0'].norm()).item() < 1e-3
 
 
+def test_capture_and_plain_forward_losses_are_bit_identical(dev):
+    """The plain forward does not store block 0's input: block 0's attn c_proj rebuilds it from the recomputed x0 (the
+    embedding kernel's operations). The capture stores it and reads it back. The per-token losses of the two paths
+    must be the same bits."""
+    print('dust capture vs plain forward B=2 T=256', flush=True)
+    from noise_amd.dust import Dust
+    from noise_amd.population import run_forward
+    ocfg, w, st, model = _setup(dev)
+    idx, tg = st['idx'].to(dev), st['targets'].to(dev)
+    clean = Dust(model).capture(idx, tg)
+    b, T = idx.shape
+    seq = torch.arange(b, dtype=torch.int32, device=dev)
+    out = run_forward(model, idx.contiguous(), tg.contiguous(), member_seq=seq, want_tokens=True, want_sum=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out['token_loss'].view(b, T), clean)
+
+
 @pytest.mark.parametrize('entry,sites', [
     (None, ['transformer.wte']),
     (0, ['o@0']),
