@@ -173,8 +173,24 @@ __global__ __launch_bounds__(256) void shared_u_kernel(const bf16_t* __restrict_
   }
 }
 
-// The 256 x 256 tile of 4 waves of 128 x 128 that both shared-x epilogues take.
+// The 256 x 256 tile of 4 waves of 128 x 128 that both shared-x epilogues take: 64-deep K steps in two LDS stages
+// when `in` allows (config 2, alternating builds on one box: the expansion kernel 0.100 against 0.102 ms, the
+// per-element one 0.513 against 0.524), 32-deep steps in four otherwise.
 using LTile = GemmShape<256, 256, 32, 2, 2>;
+using LTile64 = GemmShape<256, 256, 64, 2, 2, 2>;
+
+template <class Epi>
+static hipError_t launch_shared_gemm(const uint16_t* x, const uint16_t* w, int64_t T, int64_t in, int64_t out,
+                                     const Epi& epi, hipStream_t stream) {
+  if (in % LTile64::BK == 0) {
+    const hipError_t e = prepare_gemm<LTile64, Epi>();
+    if (e != hipSuccess) return e;
+    return launch_gemm<LTile64>((const bf16_t*)x, in, (const bf16_t*)w, in, (int)T, (int)out, (int)in, epi, stream);
+  }
+  const hipError_t e = prepare_gemm<LTile, Epi>();
+  if (e != hipSuccess) return e;
+  return launch_gemm<LTile>((const bf16_t*)x, in, (const bf16_t*)w, in, (int)T, (int)out, (int)in, epi, stream);
+}
 
 // The expansion: per tile, c2[tile] = sum of c^2 over the rounded tile, and cross[tile, i] = sum_c a_i[c] E_i[c] with
 // E_i[c] = sum_r u_i[r] c[r, c] over the tile's rows.
@@ -522,23 +538,17 @@ static int lowrank_shared_run(const uint16_t* x, int32_t mode, const uint16_t* w
   if (direct) {
     if (y) {
       EpiSharedDirect<true> epi{ws.u, ws.am, sign, ws.part, y, (int)T, (int)m, (int)out};
-      NOISE_CHECK_HIP((prepare_gemm<LTile, EpiSharedDirect<true>>()));
       NoiseTimer tm(timed ? kTimeLowrank : -1, stream);
-      NOISE_CHECK_HIP((launch_gemm<LTile>((const bf16_t*)x, in, (const bf16_t*)w, in, (int)T, (int)out, (int)in, epi,
-                                          stream)));
+      NOISE_CHECK_HIP(launch_shared_gemm(x, w, T, in, out, epi, stream));
     } else {
       EpiSharedDirect<false> epi{ws.u, ws.am, sign, ws.part, nullptr, (int)T, (int)m, (int)out};
-      NOISE_CHECK_HIP((prepare_gemm<LTile, EpiSharedDirect<false>>()));
       NoiseTimer tm(timed ? kTimeLowrank : -1, stream);
-      NOISE_CHECK_HIP((launch_gemm<LTile>((const bf16_t*)x, in, (const bf16_t*)w, in, (int)T, (int)out, (int)in, epi,
-                                          stream)));
+      NOISE_CHECK_HIP(launch_shared_gemm(x, w, T, in, out, epi, stream));
     }
   } else {
     EpiSharedExpansion epi{ws.u, ws.at, ws.c2, ws.part, (int)T, mp};
-    NOISE_CHECK_HIP((prepare_gemm<LTile, EpiSharedExpansion>()));
     NoiseTimer tm(timed ? kTimeLowrank : -1, stream);
-    NOISE_CHECK_HIP((launch_gemm<LTile>((const bf16_t*)x, in, (const bf16_t*)w, in, (int)T, (int)out, (int)in, epi,
-                                        stream)));
+    NOISE_CHECK_HIP(launch_shared_gemm(x, w, T, in, out, epi, stream));
   }
   if (sumsq) {
     NoiseTimer tm(timed ? kTimeLowrankPost : -1, stream);
