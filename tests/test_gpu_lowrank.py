@@ -63,6 +63,26 @@ def test_shared_modes_agree_and_y(dev):
     assert ((s2.double() - (y * y).sum((1, 2))).abs() / s2.double()).max().item() < 1e-5
 
 
+def test_shared_gemm_is_the_same_bits_for_32_and_64_deep_k_steps(dev):
+    """in = 512 takes the GEMM with 64-deep K steps (two LDS stages), in = 544 -- the same x and W with 32 zero
+    columns appended -- the one with 32-deep steps (four stages): the same 16-deep MFMA products in the same order,
+    plus exact zeros, so x W^T comes out with the same bits. (The signs are 0: the rank-1 term's x . b is summed by
+    another kernel whose order depends on the width.)"""
+    from noise_amd.population import lowrank
+    T, n_in, n_out, m, pad = 512, 512, 512, 2, 32
+    print(f'lowrank shared BK64 vs BK32 T={T} in={n_in}+{pad} out={n_out}', flush=True)
+    x, W, rows, a_off, b_off, a, b = _inputs(T, n_in, n_out, m, seed=4)
+    sign = torch.zeros(m)
+    zx, zw = torch.zeros(T, pad, dtype=torch.bfloat16), torch.zeros(n_out, pad, dtype=torch.bfloat16)
+    y64 = lowrank(x.to(dev), W.to(dev), a.to(dev), b.to(dev), sign.to(dev))
+    y32 = lowrank(torch.cat([x, zx], 1).to(dev), torch.cat([W, zw], 1).to(dev), a.to(dev),
+                  torch.cat([b, torch.zeros(m, pad)], 1).to(dev), sign.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(y64, y32)
+    c = (x.float() @ W.float().t()).bfloat16()
+    assert ((y64[0].float().cpu() - c.float()).abs() <= 2.0 ** -7 * c.float().abs() + 1e-6).all()
+
+
 def test_shared_sumsq_config2(dev):
     """Config 2 at full size: X [32768, 512], W [2048, 512] N(0, 0.02), 64 members, sigma 1e-3; members 0 and 37
     against the float64 oracle, every member's two evaluations against each other."""
